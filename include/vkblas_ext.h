@@ -1,0 +1,88 @@
+/*
+ * vkblas_ext.h — stream-aware entry points of the MI355X-native vkblas.
+ *
+ * The reference has no counterpart for these: its engine was synchronous and
+ * stream-less (src/vkblas.h:27-77) and its hipBLAS shim synchronised the
+ * caller's stream before and after every call (src/vkblas_hipblas.c:232).
+ * They exist so that the hipBLAS shim can launch on the handle's stream with
+ * alpha / beta possibly in device memory, and so that callers with their own
+ * stream (tests, benchmarks, PyTorch via ctypes) get the same kernels.
+ */
+#pragma once
+#include "vkblas.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum { VKBLAS_DT_F32 = 0, VKBLAS_DT_F16 = 1 } vkblas_dtype_t;
+
+/* How alpha / beta are passed (hipBLAS pointer modes). */
+typedef enum {
+    VKBLAS_SCALAR_HOST = 0,     /* the float alpha / beta arguments          */
+    VKBLAS_SCALAR_DEV_F32 = 1,  /* alpha_dev / beta_dev point to device f32  */
+    VKBLAS_SCALAR_DEV_F16 = 2   /* alpha_dev / beta_dev point to device f16  */
+} vkblas_scalar_mode_t;
+
+/* Kernel path chosen for a call (vkblas_last_path, vkblas_plan_gemm). */
+typedef enum {
+    VKBLAS_PATH_NONE = 0,
+    VKBLAS_PATH_TILE64 = 1,   /* blocked MFMA GEMM,  64 x  64 tiles        */
+    VKBLAS_PATH_TILE128 = 2,  /* blocked MFMA GEMM, 128 x 128 tiles        */
+    VKBLAS_PATH_TILE256 = 3,  /* blocked MFMA GEMM, 256 x 256 tiles        */
+    VKBLAS_PATH_SPLITK = 4,   /* split-K pass 1 + deterministic reduce     */
+    VKBLAS_PATH_SKINNY = 5    /* bandwidth-bound skinny fp16 (M <= 16)     */
+} vkblas_path_t;
+
+typedef struct {
+    int path;              /* vkblas_path_t                                 */
+    int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256)  */
+    uint32_t split;        /* split-K factor, 1 = no split                  */
+    uint32_t k_per_split;  /* K per split (multiple of the tile's K step)   */
+} vkblas_plan_t;
+
+/*
+ * General GEMM on a caller-chosen HIP stream (NULL = null stream).
+ *   ab_type: type of A and B; c_type: type of C
+ *     (F32, F32) | (F16, F16) | (F16, F32).  fp32 accumulation throughout.
+ *   split_k: 0 = heuristic, 1 = never split, >1 = force that many K slices
+ *            (clamped so every slice is non-empty).
+ * Returns VKBLAS_OK, VKBLAS_ERR_PARAM (bad arguments / unsupported type
+ * combination) or VKBLAS_ERR_INIT (no GPU, launch failure).  Asynchronous:
+ * C is valid once the stream reaches this point.
+ */
+vkblas_status_t vkblas_gemm_async(
+    vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+    vkblas_op_t op_a, vkblas_op_t op_b,
+    uint32_t M, uint32_t N, uint32_t K,
+    float alpha,
+    const void* A, uint32_t lda,
+    const void* B, uint32_t ldb,
+    float beta,
+    void* C, uint32_t ldc,
+    uint32_t batch,
+    int64_t stride_a, int64_t stride_b, int64_t stride_c,
+    vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
+    uint32_t split_k,
+    void* stream);
+
+/* The path planned for a call with these arguments (no GPU needed).
+ * aligned: A, B, C base pointers 16-byte aligned (the skinny kernel needs it).
+ * Returns VKBLAS_OK or VKBLAS_ERR_PARAM. */
+vkblas_status_t vkblas_plan_gemm(
+    vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+    vkblas_op_t op_a, vkblas_op_t op_b,
+    uint32_t M, uint32_t N, uint32_t K,
+    uint32_t lda, uint32_t ldb, uint32_t ldc,
+    uint32_t batch, uint32_t split_k, int aligned,
+    vkblas_plan_t* plan);
+
+/* Path taken by the calling thread's most recent successful GEMM call. */
+int vkblas_last_path(void);
+
+/* Library version string. */
+const char* vkblas_version(void);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,267 @@
+/*
+ * oracle/ref_gemm.c — CPU restatement of the reference's GEMM oracles.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this code, and only as the checker
+ * or the timed CPU comparator; the library never calls it and has no CPU
+ * fallback.
+ *
+ * Functions and the reference code each one follows:
+ *   oracle_ref_gemm_cm     test/test_gemm.c:32-58  (ref_gemm): hipBLAS
+ *                          column-major semantics, double accumulation,
+ *                          C = alpha * (float)s + beta * C, optional uniform
+ *                          row sampling (rows r*m/sample, last row m-1).
+ *   oracle_fill_test_gemm  test/test_gemm.c:70-73: srand(seed), then A, B, C
+ *                          filled with (rand() % 200 - 100) / 10.0f.
+ *   oracle_ref_gemm_f16_rm test/test_h.c:63-79 (cpu_ref, fp16 branch):
+ *                          row-major engine contract on fp16 bit patterns,
+ *                          double accumulation, old C read only if beta != 0,
+ *                          result rounded to fp16.  Rounding here is IEEE
+ *                          round-to-nearest-even (the reference's own f2h,
+ *                          test/test_h.c:23-41, rounds ties up; the GPU
+ *                          kernels round to nearest even, so the oracle does).
+ *   oracle_ref_gemm_f32_rm fp32 on the row-major engine contract
+ *                          (src/vkblas.h:21-26): same arithmetic as
+ *                          oracle_ref_gemm_cm, except that beta == 0 never
+ *                          reads C.  oracle_ref_gemm_cm keeps the reference's
+ *                          beta * C term even for beta == 0, as ref_gemm does.
+ *   oracle_ref_gemm_f16f32_rm  as oracle_ref_gemm_f16_rm with an fp32 result (GemmEx 16F->32F;
+ *                          no reference counterpart, same arithmetic).
+ *   oracle_fill_test_h     test/test_h.c:102, 111-113: after srand(seed),
+ *                          values (float)rand()/RAND_MAX*2-1 converted to fp16
+ *                          with ties rounded away from zero, which is what the
+ *                          reference's f2h computes for these finite inputs.
+ *   oracle_f2h_rne / oracle_h2f  IEEE binary16 conversions.
+ *
+ * The *_omp variants split the same arithmetic over output columns with
+ * OpenMP (each output is still computed by one thread in the same order).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------ fp16 bits */
+
+float oracle_h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu, man = h & 0x3ffu, u;
+    if (exp == 0) {
+        if (man == 0) {
+            u = sign;
+        } else { /* subnormal: value = man * 2^-24 */
+            int e = 0;
+            while (!(man & 0x400u)) { man <<= 1; ++e; }
+            u = sign | ((uint32_t)(113 - e) << 23) | ((man & 0x3ffu) << 13);
+        }
+    } else if (exp == 31) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else {
+        u = sign | ((exp + 112u) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* f32 -> f16 with rounding mode: 0 = nearest-even, 1 = nearest, ties away from zero */
+static uint16_t f2h_mode(float f, int ties_away) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t exp = (u >> 23) & 0xffu, man = u & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));
+    int e = (int)exp - 127; /* unbiased */
+    if (e > 15) return (uint16_t)(sign | 0x7c00u);
+    uint32_t full = man | (exp ? 0x800000u : 0u); /* 24-bit significand */
+    /* value = full * 2^(e-23) (exp != 0).  Target quantum: 2^-24 for
+     * subnormal halves (e < -14), else 2^(e-10). */
+    int shift; /* bits of full dropped */
+    if (exp == 0) return sign; /* f32 subnormals are far below half's range */
+    if (e < -14) shift = 13 + (-14 - e); else shift = 13;
+    if (shift > 24) return sign;
+    uint32_t q = full >> shift;
+    uint32_t rem = full & ((1u << shift) - 1u);
+    uint32_t halfway = 1u << (shift - 1);
+    if (rem > halfway || (rem == halfway && (ties_away || (q & 1u)))) q++;
+    uint32_t bits;
+    if (e < -14) {
+        bits = q; /* subnormal (may round up into the smallest normal: q = 0x400) */
+    } else {
+        /* q holds 1.man in 11 bits; a carry to 0x800 bumps the exponent */
+        uint32_t he = (uint32_t)(e + 15);
+        if (q & 0x800u) { q >>= 1; he++; }
+        if (he >= 31) return (uint16_t)(sign | 0x7c00u);
+        bits = (he << 10) | (q & 0x3ffu);
+    }
+    return (uint16_t)(sign | bits);
+}
+
+uint16_t oracle_f2h_rne(float f) { return f2h_mode(f, 0); }
+uint16_t oracle_f2h_ties_away(float f) { return f2h_mode(f, 1); }
+
+void oracle_f2h_rne_array(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_f2h_rne(x[i]);
+}
+void oracle_h2f_array(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_h2f(x[i]);
+}
+
+/* ------------------------------------------------------------- generators */
+
+void oracle_fill_test_gemm(unsigned seed, float* A, int64_t na, float* B, int64_t nb, float* C, int64_t nc) {
+    srand(seed);
+    for (int64_t i = 0; i < na; ++i) A[i] = (float)(rand() % 200 - 100) / 10.0f;
+    for (int64_t i = 0; i < nb; ++i) B[i] = (float)(rand() % 200 - 100) / 10.0f;
+    for (int64_t i = 0; i < nc; ++i) C[i] = (float)(rand() % 200 - 100) / 10.0f;
+}
+
+void oracle_fill_test_h(unsigned seed, uint16_t* A, int64_t na, uint16_t* B, int64_t nb, uint16_t* C,
+                        int64_t nc) {
+    srand(seed);
+    for (int64_t i = 0; i < na; ++i) A[i] = oracle_f2h_ties_away((float)rand() / RAND_MAX * 2.0f - 1.0f);
+    for (int64_t i = 0; i < nb; ++i) B[i] = oracle_f2h_ties_away((float)rand() / RAND_MAX * 2.0f - 1.0f);
+    for (int64_t i = 0; i < nc; ++i) C[i] = oracle_f2h_ties_away((float)rand() / RAND_MAX * 2.0f - 1.0f);
+}
+
+/* ---------------------------------------------------- fp32 column-major */
+
+/* rows[] gets the sampled row indices; returns their count */
+int oracle_sample_rows(int m, int sample, int* rows) {
+    if (sample <= 0 || sample >= m) {
+        for (int i = 0; i < m; ++i) rows[i] = i;
+        return m;
+    }
+    for (int r = 0; r < sample; ++r) rows[r] = (int)((int64_t)r * m / sample);
+    rows[sample - 1] = m - 1;
+    return sample;
+}
+
+static void ref_cm_col(int ta, int tb, int i, int j, int k, float alpha, const float* A, int64_t lda,
+                       const float* B, int64_t ldb, float beta, float* C, int64_t ldc) {
+    double s = 0.0;
+    for (int t = 0; t < k; ++t) {
+        float av = ta ? A[t + (int64_t)i * lda] : A[i + (int64_t)t * lda];
+        float bv = tb ? B[j + (int64_t)t * ldb] : B[t + (int64_t)j * ldb];
+        s += (double)av * bv;
+    }
+    C[i + (int64_t)j * ldc] = alpha * (float)s + beta * C[i + (int64_t)j * ldc];
+}
+
+/* ta / tb: 0 = N, 1 = T (hipBLAS transA / transB) */
+void oracle_ref_gemm_cm_omp(int ta, int tb, int m, int n, int k, float alpha, const float* A, int64_t lda,
+                            const float* B, int64_t ldb, float beta, float* C, int64_t ldc, int sample,
+                            int threads) {
+    int* rows = (int*)malloc(sizeof(int) * (size_t)(m > 0 ? m : 1));
+    int nr = oracle_sample_rows(m, sample, rows);
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+    for (int j = 0; j < n; ++j)
+        for (int ri = 0; ri < nr; ++ri) ref_cm_col(ta, tb, rows[ri], j, k, alpha, A, lda, B, ldb, beta, C, ldc);
+    free(rows);
+    (void)threads;
+}
+
+void oracle_ref_gemm_cm(int ta, int tb, int m, int n, int k, float alpha, const float* A, int64_t lda,
+                        const float* B, int64_t ldb, float beta, float* C, int64_t ldc, int sample) {
+    int* rows = (int*)malloc(sizeof(int) * (size_t)(m > 0 ? m : 1));
+    int nr = oracle_sample_rows(m, sample, rows);
+    for (int ri = 0; ri < nr; ++ri)
+        for (int j = 0; j < n; ++j) ref_cm_col(ta, tb, rows[ri], j, k, alpha, A, lda, B, ldb, beta, C, ldc);
+    free(rows);
+}
+
+/* ------------------------------------------------------ fp16 row-major */
+
+/* fp16 -> fp32 table (filled before any parallel region) */
+static float g_h2f_lut[65536];
+static int g_h2f_ready = 0;
+static void h2f_lut_init(void) {
+    if (g_h2f_ready) return;
+    for (uint32_t i = 0; i < 65536u; ++i) g_h2f_lut[i] = oracle_h2f((uint16_t)i);
+    g_h2f_ready = 1;
+}
+
+static double dot_f16(int op_a, int op_b, int m, int n, int K, const uint16_t* A, int64_t lda,
+                      const uint16_t* B, int64_t ldb) {
+    double s = 0.0;
+    for (int k = 0; k < K; ++k) {
+        float av = op_a ? g_h2f_lut[A[(int64_t)k * lda + m]] : g_h2f_lut[A[(int64_t)m * lda + k]];
+        float bv = op_b ? g_h2f_lut[B[(int64_t)n * ldb + k]] : g_h2f_lut[B[(int64_t)k * ldb + n]];
+        s += (double)av * bv;
+    }
+    return s;
+}
+
+/* op_a / op_b: engine ops (0 = N, 1 = T); rows: optional list of the rows m
+ * to compute (NULL = all M) */
+void oracle_ref_gemm_f16_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
+                            const uint16_t* B, int64_t ldb, float alpha, float beta, uint16_t* C, int64_t ldc,
+                            const int* rows, int nrows, int threads) {
+    int nr = rows ? nrows : M;
+    h2f_lut_init();
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
+#endif
+    for (int ri = 0; ri < nr; ++ri) {
+        for (int n = 0; n < N; ++n) {
+            const int m = rows ? rows[ri] : ri;
+            double s = dot_f16(op_a, op_b, m, n, K, A, lda, B, ldb);
+            float old = beta != 0.0f ? oracle_h2f(C[(int64_t)m * ldc + n]) : 0.0f;
+            C[(int64_t)m * ldc + n] = oracle_f2h_rne(alpha * (float)s + beta * old);
+        }
+    }
+    (void)threads;
+}
+
+void oracle_ref_gemm_f16f32_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
+                               const uint16_t* B, int64_t ldb, float alpha, float beta, float* C, int64_t ldc,
+                               const int* rows, int nrows, int threads) {
+    int nr = rows ? nrows : M;
+    h2f_lut_init();
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
+#endif
+    for (int ri = 0; ri < nr; ++ri) {
+        for (int n = 0; n < N; ++n) {
+            const int m = rows ? rows[ri] : ri;
+            double s = dot_f16(op_a, op_b, m, n, K, A, lda, B, ldb);
+            float old = beta != 0.0f ? C[(int64_t)m * ldc + n] : 0.0f;
+            C[(int64_t)m * ldc + n] = alpha * (float)s + beta * old;
+        }
+    }
+    (void)threads;
+}
+
+/* fp32 row-major engine contract (src/vkblas.h:21-26), same arithmetic as
+ * oracle_ref_gemm_cm; used to check engine-API calls directly. */
+void oracle_ref_gemm_f32_rm(int op_a, int op_b, int M, int N, int K, const float* A, int64_t lda, const float* B,
+                            int64_t ldb, float alpha, float beta, float* C, int64_t ldc, const int* rows,
+                            int nrows, int threads) {
+    int nr = rows ? nrows : M;
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
+#endif
+    for (int ri = 0; ri < nr; ++ri) {
+        for (int n = 0; n < N; ++n) {
+            const int m = rows ? rows[ri] : ri;
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) {
+                float av = op_a ? A[(int64_t)k * lda + m] : A[(int64_t)m * lda + k];
+                float bv = op_b ? B[(int64_t)n * ldb + k] : B[(int64_t)k * ldb + n];
+                s += (double)av * bv;
+            }
+            float old = beta != 0.0f ? C[(int64_t)m * ldc + n] : 0.0f;
+            C[(int64_t)m * ldc + n] = alpha * (float)s + beta * old;
+        }
+    }
+    (void)threads;
+}

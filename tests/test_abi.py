@@ -1,0 +1,150 @@
+"""CPU tests of the drop-in boundary: the C-ABI library loads, exports every
+symbol include/*.h declares, and its host logic (argument checks, path
+planning) behaves as documented.  No kernel is launched here."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import vkblas_amd as vk
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(REPO, "include")
+
+
+def declared_functions(header):
+    text = open(os.path.join(INCLUDE, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s+\**\s*([A-Za-z_]\w*)\s*\(", text, flags=re.M))
+    names = {n for n in names if n.startswith(("vkblas_", "hipblas"))}
+    for decl, s, d, c, z in re.findall(r"^VKBLAS_FOUR\((\w+),\s*(\w+),\s*(\w+),\s*(\w+),\s*(\w+)\)", text, flags=re.M):
+        for base in (s, d, c, z):
+            names.add("hipblas" + base)
+        names.add("hipblas" + c + "_v2")
+        names.add("hipblas" + z + "_v2")
+    return names
+
+
+def exported_symbols():
+    out = subprocess.run(["nm", "-D", "--defined-only", vk.LIB_PATH], check=True, capture_output=True, text=True)
+    return {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+
+
+def test_library_loads():
+    L = vk.load()
+    assert vk.version().startswith("vkblas-mi355x")
+    assert L is vk.load()
+
+
+@pytest.mark.parametrize("header", ["vkblas.h", "vkblas_ext.h", "vkblas_hipblas.h"])
+def test_exports_every_declared_symbol(header):
+    names = declared_functions(header)
+    assert len(names) > 3, names
+    missing = sorted(names - exported_symbols())
+    assert not missing, missing
+
+
+def test_reference_export_set_present():
+    """Symbols the reference's tests and PyTorch bind (test_gemm.c:212-215,
+    test_h.c:84-86, test_v9h.c:51-52 and 144, src/vkblas_hipblas.c)."""
+    want = {"hipblasSgemm", "hipblasCreate", "hipblasDestroy", "hipblasSgemmStridedBatched", "vkblas_gemm_bf16",
+            "vkblas_gemm_f16", "vkblas_gemm_f32", "hipblasGemmEx", "hipblasGemmStridedBatchedEx_v2",
+            "hipblasGemmEx_v2", "hipblasSetStream", "hipblasGetStream", "hipblasSetPointerMode",
+            "hipblasGetPointerMode", "hipblasSetWorkspace", "vkblas_cache_invalidate_base",
+            "hipblasHgemm", "hipblasHgemmStridedBatched", "hipblasGemmStridedBatchedEx"}
+    assert not (want - exported_symbols())
+
+
+def test_no_free_interposition():
+    """The library must not export hipFree & co (no import cache to flush)."""
+    assert not ({"hipFree", "hipHostFree", "hipFreeManaged"} & exported_symbols())
+
+
+def test_no_cuda_or_oracle_dependency():
+    out = subprocess.run(["readelf", "-d", vk.LIB_PATH], check=True, capture_output=True, text=True).stdout
+    needed = re.findall(r"\[(.*?)\]", "\n".join(l for l in out.splitlines() if "NEEDED" in l))
+    assert any(n.startswith("libamdhip64") for n in needed)
+    assert not any("oracle" in n or "cuda" in n or "hipblas" in n for n in needed), needed
+
+
+# --------------------------------------------------------------- planning
+
+P = vk.plan
+
+
+def test_plan_rejects_bad_arguments():
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 0, 0, 0, 4, 4, 4, 4, 4)          # M == 0
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 4, 4, 4, 4, 4, batch=0)
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 4, 8, 4, 8, 4)          # lda < K (op_a = N)
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 1, 0, 8, 4, 4, 4, 4, 4)          # lda < M (op_a = T)
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8, 4, 4, 4, 8)          # ldb < N (op_b = N)
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8, 4, 4, 8, 4)          # ldc < N
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_F32, vk.DT_F16, 0, 0, 4, 4, 4, 4, 4, 4)          # f32 in, f16 out: unsupported
+
+
+def test_engine_param_errors_without_gpu():
+    """Argument errors are reported before any device work (same codes as the
+    reference: zero dims -> VKBLAS_ERR_PARAM, src/vkblas.c:3114)."""
+    p = 4096
+    assert vk.gemm_f32(0, 0, 0, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
+    assert vk.gemm_f16(0, 0, 4, 4, 4, 1.0, None, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
+    assert vk.load().vkblas_gemm_bf16(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, 1, 0, 0, 0) == vk.ERR_INIT
+    for name in ("vkblas_gemm_c64", "vkblas_gemm_f64", "vkblas_gemm_z64"):
+        assert hasattr(vk.load(), name)
+
+
+def test_plan_headline_configs():
+    # config 2: fp32 4096^3 -> one 256x256 tile per CU
+    for oa in (0, 1):
+        for ob in (0, 1):
+            pl = P(vk.DT_F32, vk.DT_F32, oa, ob, 4096, 4096, 4096, 4096, 4096, 4096)
+            assert pl.path == vk.PATH_TILE256 and pl.split == 1
+    # config 3: fp16 GEMMs
+    for n in (2048, 4096, 8192):
+        assert P(vk.DT_F16, vk.DT_F16, 0, 0, n, n, n, n, n, n).path in (vk.PATH_TILE128, vk.PATH_TILE256)
+    # config 4: decode (engine op_a = N, op_b = T, M = tokens)
+    for ntok in (1, 4, 8, 16):
+        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192)
+        assert pl.path == vk.PATH_SKINNY
+    # not skinny when misaligned, batched, or fp32
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, aligned=False).path != vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, batch=2).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    # config 5b: batched 64 x 512^3
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 512, 512, 512, 512, 512, 512, batch=64).split == 1
+
+
+@pytest.mark.parametrize("K", [65536, 262144])
+@pytest.mark.parametrize("split", [4, 16, 64])
+@pytest.mark.parametrize("dt", [vk.DT_F32, vk.DT_F16])
+def test_plan_forced_split(K, split, dt):
+    """config 5a: forced split factors; slices cover K exactly once, each
+    slice a whole number of K steps and non-empty."""
+    pl = P(dt, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256, split_k=split)
+    assert pl.path == vk.PATH_SPLITK
+    bk = 64 if dt == vk.DT_F16 else 32
+    assert pl.k_per_split % bk == 0
+    assert pl.split * pl.k_per_split >= K > (pl.split - 1) * pl.k_per_split
+    assert pl.split == split
+
+
+def test_plan_split_heuristic_and_off():
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256)
+    assert pl.path == vk.PATH_SPLITK and 2 <= pl.split <= 64
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=1)
+    assert pl.path != vk.PATH_SPLITK
+    # batched calls never split
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, batch=2, split_k=8)
+    assert pl.split == 1
+    # split count clamps so no slice is empty
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 64, 64, 100, 100, 64, 64, split_k=64)
+    assert pl.split * pl.k_per_split >= 100 > (pl.split - 1) * pl.k_per_split

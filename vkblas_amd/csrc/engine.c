@@ -1,0 +1,352 @@
+/*
+ * engine.c — host dispatcher of the MI355X-native vkblas (C11).
+ *
+ * Implements the public API of include/vkblas.h and include/vkblas_ext.h on
+ * top of the HIP launch layer (vkb_launch.h).  It replaces the reference's
+ * Vulkan engine entry points vkblas_gemm_f32 (src/vkblas.c:3104-3341) and
+ * vkblas_gemm_f16 (src/vkblas.c:3517-3651) and their path selection
+ * (pick_tile128 src/vkblas.c:914-928, split-K gates src/vkblas.c:2850-2867 and
+ * 1636-1668, M==1 matvec gates src/vkblas.c:3122-3161 and 3535-3559).
+ *
+ * Differences by design:
+ *   - no global lock: the only shared state is initialised once
+ *     (pthread_once) and the split-K workspace comes from a stream-ordered
+ *     memory pool, so concurrent calls on different streams never share it;
+ *   - launches are asynchronous on the caller's stream;
+ *   - every TA/TB variant runs natively (no transposed copies, no cache).
+ */
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <hip/hip_runtime_api.h>
+
+#include "vkblas_ext.h"
+#include "vkb_launch.h"
+
+#define VKBLAS_VERSION_STRING "vkblas-mi355x 0.1.0 (gfx950)"
+
+/* ------------------------------------------------------------------ state */
+
+#define VKB_MAX_DEVICES 64
+
+static pthread_once_t g_once = PTHREAD_ONCE_INIT;
+static int g_ndev = 0;          /* visible devices, 0 = no GPU */
+static int g_trace = 0;         /* VKBLAS_TRACE */
+static int g_force_tile = -1;   /* VKBLAS_TILE = 64 | 128 | 256 */
+static uint32_t g_force_split = 0; /* VKBLAS_SPLITK = n (applies when split_k == 0) */
+static int g_no_skinny = 0;     /* VKBLAS_NO_SKINNY = 1 */
+
+static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
+static hipMemPool_t g_pool[VKB_MAX_DEVICES];
+
+static __thread int g_last_path = VKBLAS_PATH_NONE;
+
+static void init_once(void) {
+    const char* e;
+    g_trace = (e = getenv("VKBLAS_TRACE")) != NULL && e[0] && e[0] != '0';
+    if ((e = getenv("VKBLAS_TILE")) != NULL) {
+        int v = atoi(e);
+        g_force_tile = v == 64 ? VKB_TILE_64 : v == 128 ? VKB_TILE_128 : v == 256 ? VKB_TILE_256 : -1;
+    }
+    if ((e = getenv("VKBLAS_SPLITK")) != NULL) {
+        long v = atol(e);
+        g_force_split = v > 0 ? (uint32_t)v : 0;
+    }
+    g_no_skinny = (e = getenv("VKBLAS_NO_SKINNY")) != NULL && e[0] == '1';
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+    g_ndev = n;
+    if (g_trace) fprintf(stderr, "[vkblas] init: %s, %d device(s)\n", VKBLAS_VERSION_STRING, n);
+}
+
+static int ensure_init(void) {
+    pthread_once(&g_once, init_once);
+    return g_ndev > 0;
+}
+
+/* Stream-ordered workspace for split-K partials: a private pool per device
+ * that keeps its memory between calls (release threshold = max). */
+static hipMemPool_t pool_for_current_device(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= VKB_MAX_DEVICES) return NULL;
+    pthread_mutex_lock(&g_pool_lock);
+    if (!g_pool[dev]) {
+        hipMemPoolProps props;
+        memset(&props, 0, sizeof(props));
+        props.allocType = hipMemAllocationTypePinned;
+        props.handleTypes = hipMemHandleTypeNone;
+        props.location.type = hipMemLocationTypeDevice;
+        props.location.id = dev;
+        hipMemPool_t pool = NULL;
+        if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
+            uint64_t thr = UINT64_MAX;
+            hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &thr);
+            g_pool[dev] = pool;
+        }
+    }
+    hipMemPool_t p = g_pool[dev];
+    pthread_mutex_unlock(&g_pool_lock);
+    return p;
+}
+
+/* --------------------------------------------------------------- planning */
+
+static uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+static int tile_path(int tile) {
+    return tile == VKB_TILE_256 ? VKBLAS_PATH_TILE256
+         : tile == VKB_TILE_128 ? VKBLAS_PATH_TILE128 : VKBLAS_PATH_TILE64;
+}
+
+/* Tile choice for 256 CUs: the largest tile that still gives about one
+ * workgroup per CU; smaller tiles only when the large one would starve. */
+static int choose_tile(uint32_t M, uint32_t N, uint32_t batch) {
+    if (g_force_tile >= 0) return g_force_tile;
+    uint64_t t256 = (uint64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
+    uint64_t t128 = (uint64_t)cdiv(M, 128) * cdiv(N, 128) * batch;
+    if (M >= 256 && N >= 256 && t256 >= 224) return VKB_TILE_256;
+    if (M >= 96 && N >= 96 && t128 >= 96) return VKB_TILE_128;
+    if (M > 64 && N > 64 && t128 >= 32) return VKB_TILE_128;
+    return VKB_TILE_64;
+}
+
+vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+                                 vkblas_op_t op_a, vkblas_op_t op_b,
+                                 uint32_t M, uint32_t N, uint32_t K,
+                                 uint32_t lda, uint32_t ldb, uint32_t ldc,
+                                 uint32_t batch, uint32_t split_k, int aligned,
+                                 vkblas_plan_t* plan) {
+    pthread_once(&g_once, init_once);
+    if (!plan) return VKBLAS_ERR_PARAM;
+    memset(plan, 0, sizeof(*plan));
+    if (M == 0 || N == 0 || K == 0 || batch == 0) return VKBLAS_ERR_PARAM;
+    if (!((ab_type == VKBLAS_DT_F32 && c_type == VKBLAS_DT_F32) ||
+          (ab_type == VKBLAS_DT_F16 && (c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_F32))))
+        return VKBLAS_ERR_PARAM;
+    if (lda < (op_a == VKBLAS_OP_N ? K : M)) return VKBLAS_ERR_PARAM;
+    if (ldb < (op_b == VKBLAS_OP_T ? K : N)) return VKBLAS_ERR_PARAM;
+    if (ldc < N) return VKBLAS_ERR_PARAM;
+    if (split_k == 0 && g_force_split) split_k = g_force_split;
+
+    /* decode-shaped fp16: X[M<=16, K] . W[N, K]^T, both K-contiguous */
+    if (ab_type == VKBLAS_DT_F16 && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 16 &&
+        batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && !g_no_skinny) {
+        plan->path = VKBLAS_PATH_SKINNY;
+        plan->tile = VKB_TILE_64;
+        plan->split = 1;
+        plan->k_per_split = K;
+        return VKBLAS_OK;
+    }
+
+    const uint32_t bk = vkb_tile_bk(ab_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32);
+    int tile = choose_tile(M, N, batch);
+    uint32_t split = 1;
+    if (batch == 1) {
+        if (split_k > 1) {
+            split = split_k;
+        } else if (split_k == 0) {
+            /* few output tiles and a long K: split K so ~256 workgroups run */
+            uint64_t tiles = (uint64_t)cdiv(M, vkb_tile_bm(tile)) * cdiv(N, vkb_tile_bn(tile));
+            if (tiles < 64 && K >= 4096) {
+                uint64_t want = 256 / tiles;
+                uint64_t kmax = K / (8 * bk);   /* keep >= 8 K steps per slice */
+                if (want > kmax) want = kmax;
+                if (want > 64) want = 64;
+                split = want >= 2 ? (uint32_t)want : 1;
+            }
+        }
+    }
+    if (split > 1) {
+        uint32_t kps = cdiv(cdiv(K, split), bk) * bk;
+        split = cdiv(K, kps);                     /* every slice non-empty */
+        /* cap the fp32 partials at 1 GiB */
+        while (split > 1 && (uint64_t)split * M * N * 4 > (1ull << 30)) {
+            split = (split + 1) / 2;
+            kps = cdiv(cdiv(K, split), bk) * bk;
+            split = cdiv(K, kps);
+        }
+        if (split > 1) {
+            plan->path = VKBLAS_PATH_SPLITK;
+            plan->tile = tile;
+            plan->split = split;
+            plan->k_per_split = kps;
+            return VKBLAS_OK;
+        }
+    }
+    plan->path = tile_path(tile);
+    plan->tile = tile;
+    plan->split = 1;
+    plan->k_per_split = K;
+    return VKBLAS_OK;
+}
+
+/* -------------------------------------------------------------- execution */
+
+static const char* path_name(int p) {
+    switch (p) {
+        case VKBLAS_PATH_TILE64: return "tile64";
+        case VKBLAS_PATH_TILE128: return "tile128";
+        case VKBLAS_PATH_TILE256: return "tile256";
+        case VKBLAS_PATH_SPLITK: return "splitk";
+        case VKBLAS_PATH_SKINNY: return "skinny";
+        default: return "none";
+    }
+}
+
+vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+                                  vkblas_op_t op_a, vkblas_op_t op_b,
+                                  uint32_t M, uint32_t N, uint32_t K,
+                                  float alpha,
+                                  const void* A, uint32_t lda,
+                                  const void* B, uint32_t ldb,
+                                  float beta,
+                                  void* C, uint32_t ldc,
+                                  uint32_t batch,
+                                  int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                                  vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
+                                  const void* beta_dev, uint32_t split_k, void* stream) {
+    if (!A || !B || !C) return VKBLAS_ERR_PARAM;
+    if (scalar_mode != VKBLAS_SCALAR_HOST && (!alpha_dev || !beta_dev)) return VKBLAS_ERR_PARAM;
+    if (scalar_mode != VKBLAS_SCALAR_HOST && scalar_mode != VKBLAS_SCALAR_DEV_F32 &&
+        scalar_mode != VKBLAS_SCALAR_DEV_F16)
+        return VKBLAS_ERR_PARAM;
+    const int aligned = ((uintptr_t)A % 16 == 0) && ((uintptr_t)B % 16 == 0);
+    vkblas_plan_t plan;
+    vkblas_status_t st = vkblas_plan_gemm(ab_type, c_type, op_a, op_b, M, N, K, lda, ldb, ldc,
+                                          batch, split_k, aligned, &plan);
+    if (st != VKBLAS_OK) return st;
+    if (!ensure_init()) return VKBLAS_ERR_INIT;
+
+    const int ab = ab_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32;
+    const int ct = c_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32;
+    int rc = 0;
+    if (g_trace)
+        fprintf(stderr, "[vkblas] gemm %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s split=%u\n",
+                op_a ? "T" : "N", op_b ? "T" : "N", ab == VKB_T_F16 ? "f16" : "f32",
+                ct == VKB_T_F16 ? "f16" : "f32", M, N, K, lda, ldb, ldc, batch,
+                path_name(plan.path), plan.split);
+
+    if (plan.path == VKBLAS_PATH_SKINNY) {
+        rc = vkb_launch_skinny_f16(A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
+                                   alpha_dev, beta_dev, stream);
+    } else {
+        vkb_gemm_args a;
+        memset(&a, 0, sizeof(a));
+        a.A = A; a.B = B; a.C = C;
+        a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+        a.stride_a = stride_a; a.stride_b = stride_b; a.stride_c = stride_c;
+        a.M = M; a.N = N; a.K = K;
+        a.batch = batch;
+        a.split = 1;
+        a.k_per_split = K;
+        a.a_kmajor = op_a == VKBLAS_OP_N;
+        a.b_kmajor = op_b == VKBLAS_OP_T;
+        a.ab_type = ab;
+        a.c_type = ct;
+        a.alpha = alpha; a.beta = beta;
+        a.scalar_mode = (int)scalar_mode;
+        a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
+        if (plan.path == VKBLAS_PATH_SPLITK) {
+            hipMemPool_t pool = pool_for_current_device();
+            if (!pool) return VKBLAS_ERR_INIT;
+            const size_t bytes = (size_t)plan.split * M * N * sizeof(float);
+            void* ws = NULL;
+            if (hipMallocFromPoolAsync(&ws, bytes, pool, (hipStream_t)stream) != hipSuccess) return VKBLAS_ERR_INIT;
+            a.C = ws;
+            a.ldc = N;
+            a.stride_c = 0;
+            a.c_type = VKB_T_F32;
+            a.split = plan.split;
+            a.k_per_split = plan.k_per_split;
+            a.stride_split = (int64_t)M * N;
+            a.alpha = 1.0f; a.beta = 0.0f;
+            a.scalar_mode = VKB_SCALAR_HOST;
+            a.alpha_dev = a.beta_dev = NULL;
+            rc = vkb_launch_gemm(&a, plan.tile, stream);
+            if (rc == 0)
+                rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct,
+                                              alpha, beta, (int)scalar_mode, alpha_dev, beta_dev, stream);
+            hipFreeAsync(ws, (hipStream_t)stream);
+        } else {
+            rc = vkb_launch_gemm(&a, plan.tile, stream);
+        }
+    }
+    if (rc != 0) {
+        if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s\n", hipGetErrorString((hipError_t)rc));
+        return VKBLAS_ERR_INIT;
+    }
+    g_last_path = plan.path;
+    return VKBLAS_OK;
+}
+
+int vkblas_last_path(void) { return g_last_path; }
+
+const char* vkblas_version(void) { return VKBLAS_VERSION_STRING; }
+
+/* ------------------------------------------------------ reference C API */
+
+vkblas_status_t vkblas_gemm_f32(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
+                                float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
+                                float beta, void* C, uint32_t ldc, uint32_t batch,
+                                int64_t stride_a, int64_t stride_b, int64_t stride_c) {
+    return vkblas_gemm_async(VKBLAS_DT_F32, VKBLAS_DT_F32, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta,
+                             C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL, NULL, 0,
+                             NULL);
+}
+
+vkblas_status_t vkblas_gemm_f16(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
+                                float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
+                                float beta, void* C, uint32_t ldc, uint32_t batch,
+                                int64_t stride_a, int64_t stride_b, int64_t stride_c) {
+    return vkblas_gemm_async(VKBLAS_DT_F16, VKBLAS_DT_F16, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta,
+                             C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL, NULL, 0,
+                             NULL);
+}
+
+vkblas_status_t vkblas_gemm_bf16(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
+                                 float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
+                                 float beta, void* C, uint32_t ldc, uint32_t batch,
+                                 int64_t stride_a, int64_t stride_b, int64_t stride_c) {
+    (void)op_a; (void)op_b; (void)M; (void)N; (void)K; (void)alpha; (void)A; (void)lda; (void)B;
+    (void)ldb; (void)beta; (void)C; (void)ldc; (void)batch; (void)stride_a; (void)stride_b; (void)stride_c;
+    return VKBLAS_ERR_INIT;
+}
+
+vkblas_status_t vkblas_gemm_bf16_hipblas(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N,
+                                         uint32_t K, float alpha, const void* A, uint32_t lda, const void* B,
+                                         uint32_t ldb, float beta, void* C, uint32_t ldc, uint32_t batch,
+                                         int64_t stride_a, int64_t stride_b, int64_t stride_c) {
+    return vkblas_gemm_bf16(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, stride_a,
+                            stride_b, stride_c);
+}
+
+int vkblas_gemm_c64(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K, float alpha_r,
+                    float alpha_i, const void* A, uint32_t lda, const void* B, uint32_t ldb, float beta_r,
+                    float beta_i, void* C, uint32_t ldc, uint32_t batch, int64_t stride_a, int64_t stride_b,
+                    int64_t stride_c) {
+    (void)op_a; (void)op_b; (void)M; (void)N; (void)K; (void)alpha_r; (void)alpha_i; (void)A; (void)lda;
+    (void)B; (void)ldb; (void)beta_r; (void)beta_i; (void)C; (void)ldc; (void)batch; (void)stride_a;
+    (void)stride_b; (void)stride_c;
+    return VKBLAS_ERR_INIT;
+}
+
+int vkblas_gemm_f64(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K, double alpha,
+                    const void* A, uint32_t lda, const void* B, uint32_t ldb, double beta, void* C,
+                    uint32_t ldc, uint32_t batch, int64_t stride_a, int64_t stride_b, int64_t stride_c) {
+    (void)op_a; (void)op_b; (void)M; (void)N; (void)K; (void)alpha; (void)A; (void)lda; (void)B; (void)ldb;
+    (void)beta; (void)C; (void)ldc; (void)batch; (void)stride_a; (void)stride_b; (void)stride_c;
+    return VKBLAS_ERR_INIT;
+}
+
+int vkblas_gemm_z64(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K, double alpha_r,
+                    double alpha_i, const void* A, uint32_t lda, const void* B, uint32_t ldb, double beta_r,
+                    double beta_i, void* C, uint32_t ldc, uint32_t batch, int64_t stride_a, int64_t stride_b,
+                    int64_t stride_c) {
+    (void)op_a; (void)op_b; (void)M; (void)N; (void)K; (void)alpha_r; (void)alpha_i; (void)A; (void)lda;
+    (void)B; (void)ldb; (void)beta_r; (void)beta_i; (void)C; (void)ldc; (void)batch; (void)stride_a;
+    (void)stride_b; (void)stride_c;
+    return VKBLAS_ERR_INIT;
+}
+
+void vkblas_cache_invalidate_base(const void* ptr) { (void)ptr; }

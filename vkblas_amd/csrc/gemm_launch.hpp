@@ -1,0 +1,82 @@
+// gemm_launch.hpp — host-side launcher for gemm_kernel<> (one instantiation
+// set per element-type pair; gemm_f32.hip / gemm_f16.hip include this).
+#pragma once
+#include "gemm_mfma.hpp"
+#include "vkb_launch.h"
+
+namespace vkb {
+
+template <int TILE> struct TileDim;
+template <> struct TileDim<VKB_TILE_64>  { static constexpr int BM = 64,  BN = 64;  };
+template <> struct TileDim<VKB_TILE_128> { static constexpr int BM = 128, BN = 128; };
+template <> struct TileDim<VKB_TILE_256> { static constexpr int BM = 256, BN = 256; };
+
+template <typename T, typename TC, bool AK, bool BKM, int TILE, bool CHECKED>
+static int launch_one(const KParams& p, uint32_t grid, hipStream_t st) {
+    constexpr int BM = TileDim<TILE>::BM, BN = TileDim<TILE>::BN;
+    hipLaunchKernelGGL((gemm_kernel<T, TC, AK, BKM, BM, BN, CHECKED>), dim3(grid), dim3(256), 0, st, p);
+    return (int)hipGetLastError();
+}
+
+template <typename T, typename TC, bool AK, bool BKM, int TILE>
+static int launch_ck(const KParams& p, bool checked, uint32_t grid, hipStream_t st) {
+    return checked ? launch_one<T, TC, AK, BKM, TILE, true>(p, grid, st)
+                   : launch_one<T, TC, AK, BKM, TILE, false>(p, grid, st);
+}
+
+template <typename T, typename TC, int TILE>
+static int launch_layout(const KParams& p, bool ak, bool bk, bool checked, uint32_t grid, hipStream_t st) {
+    if (ak) {
+        return bk ? launch_ck<T, TC, true, true, TILE>(p, checked, grid, st)
+                  : launch_ck<T, TC, true, false, TILE>(p, checked, grid, st);
+    }
+    return bk ? launch_ck<T, TC, false, true, TILE>(p, checked, grid, st)
+              : launch_ck<T, TC, false, false, TILE>(p, checked, grid, st);
+}
+
+static inline bool aligned(const void* ptr, uintptr_t a) { return ((uintptr_t)ptr % a) == 0; }
+
+template <typename T, typename TC>
+static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
+    constexpr int VEC = Elem<T>::VEC;
+    constexpr int BK = Elem<T>::BK;
+    int bm = 64, bn = 64;
+    if (tile == VKB_TILE_128) { bm = bn = 128; }
+    else if (tile == VKB_TILE_256) { bm = bn = 256; }
+    else if (tile != VKB_TILE_64) return (int)hipErrorInvalidValue;
+
+    KParams p;
+    p.A = a->A; p.B = a->B; p.C = a->C;
+    p.lda = a->lda; p.ldb = a->ldb; p.ldc = a->ldc;
+    p.sa = a->stride_a; p.sb = a->stride_b; p.sc = a->stride_c;
+    p.M = a->M; p.N = a->N; p.K = a->K;
+    p.batch = a->batch ? a->batch : 1;
+    p.split = a->split > 1 ? a->split : 1;
+    p.kps = p.split > 1 ? a->k_per_split : a->K;
+    p.s_split = p.split > 1 ? a->stride_split : 0;
+    p.tiles_m = (a->M + bm - 1) / bm;
+    p.tiles_n = (a->N + bn - 1) / bn;
+    p.alpha = a->alpha; p.beta = a->beta;
+    p.scalar_mode = a->scalar_mode;
+    p.alpha_dev = a->alpha_dev; p.beta_dev = a->beta_dev;
+    const bool multi = p.batch > 1;
+    p.vec_a = (a->lda % VEC == 0) && aligned(a->A, 16) && (!multi || a->stride_a % VEC == 0);
+    p.vec_b = (a->ldb % VEC == 0) && aligned(a->B, 16) && (!multi || a->stride_b % VEC == 0);
+    p.vec_c = (a->ldc % 4 == 0) && aligned(a->C, 4 * sizeof(TC)) && (!multi || a->stride_c % 4 == 0) &&
+              (p.split == 1 || p.s_split % 4 == 0);
+    if (p.split > 1 && (p.kps == 0 || p.kps % BK != 0)) return (int)hipErrorInvalidValue;
+
+    const bool full = (a->M % bm == 0) && (a->N % bn == 0) && (a->K % BK == 0) &&
+                      p.vec_a && p.vec_b && p.vec_c;
+    const uint64_t grid64 = (uint64_t)p.tiles_m * p.tiles_n * p.batch * p.split;
+    if (grid64 == 0 || grid64 > 0x7fffffffull) return (int)hipErrorInvalidValue;
+    const uint32_t grid = (uint32_t)grid64;
+    const bool ak = a->a_kmajor != 0, bk = a->b_kmajor != 0;
+    switch (tile) {
+        case VKB_TILE_64:  return launch_layout<T, TC, VKB_TILE_64>(p, ak, bk, !full, grid, st);
+        case VKB_TILE_128: return launch_layout<T, TC, VKB_TILE_128>(p, ak, bk, !full, grid, st);
+        default:           return launch_layout<T, TC, VKB_TILE_256>(p, ak, bk, !full, grid, st);
+    }
+}
+
+}  // namespace vkb

@@ -1,0 +1,87 @@
+/*
+ * vkb_launch.h — internal C ABI between the host dispatcher (engine.c, C11)
+ * and the gfx950 HIP kernels (*.hip).  Plain pointers, sizes and scalars
+ * only; every launcher enqueues on the given stream and returns 0 on success
+ * or a hipError_t value.
+ *
+ * Operand convention (row-major engine contract, reference src/vkblas.h:21-26):
+ *   C[M,N] = alpha * A_eff[M,K] @ B_eff[K,N] + beta * C
+ *   a_kmajor = (op_a == N): A row m is K-contiguous  (A[m*lda + k])
+ *              otherwise     A column is M-contiguous (A[k*lda + m])
+ *   b_kmajor = (op_b == T): B row n is K-contiguous  (B[n*ldb + k])
+ *              otherwise     B row k is N-contiguous  (B[k*ldb + n])
+ */
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types (values match vkblas_dtype_t in vkblas_ext.h) */
+enum { VKB_T_F32 = 0, VKB_T_F16 = 1 };
+
+/* how alpha / beta reach the kernel */
+enum { VKB_SCALAR_HOST = 0, VKB_SCALAR_DEV_F32 = 1, VKB_SCALAR_DEV_F16 = 2 };
+
+/* GEMM tile configurations (block tile BM x BN, 4 waves, BK = 128 bytes) */
+enum {
+    VKB_TILE_64  = 0,  /*  64 x  64, waves 2x2 of  32x32 */
+    VKB_TILE_128 = 1,  /* 128 x 128, waves 2x2 of  64x64 */
+    VKB_TILE_256 = 2,  /* 256 x 256, waves 2x2 of 128x128 */
+    VKB_TILE_COUNT = 3
+};
+
+typedef struct vkb_gemm_args {
+    const void* A;
+    const void* B;
+    void* C;
+    int64_t lda, ldb, ldc;
+    int64_t stride_a, stride_b, stride_c;  /* per batch, elements */
+    uint32_t M, N, K;
+    uint32_t batch;
+    /* split-K pass 1: split > 1 writes raw fp32 partial sums of K-slice s
+     * (k in [s*k_per_split, min(K,(s+1)*k_per_split))) to
+     * C + s*stride_split with alpha = 1, beta = 0. */
+    uint32_t split;
+    uint32_t k_per_split;
+    int64_t stride_split;
+    int a_kmajor, b_kmajor;
+    int ab_type, c_type;
+    float alpha, beta;
+    int scalar_mode;
+    const void* alpha_dev;
+    const void* beta_dev;
+} vkb_gemm_args;
+
+/* Tile-config properties the dispatcher plans with. */
+uint32_t vkb_tile_bm(int tile);
+uint32_t vkb_tile_bn(int tile);
+/* K granularity of one LDS stage for an element type (128 bytes of K). */
+uint32_t vkb_tile_bk(int ab_type);
+
+/* Blocked MFMA GEMM for all four layouts.  ab_type F32 -> c_type F32;
+ * ab_type F16 -> c_type F16 or F32. */
+int vkb_launch_gemm(const vkb_gemm_args* a, int tile, void* stream);
+
+/* Split-K pass 2: C = alpha * sum_{s=0}^{split-1} P[s] + beta * C, summed in
+ * that fixed order (deterministic).  P[s] is M x N fp32, row pitch N,
+ * P[s] = P + s*stride_split. */
+int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t split,
+                             uint32_t M, uint32_t N, void* C, int64_t ldc, int c_type,
+                             float alpha, float beta, int scalar_mode,
+                             const void* alpha_dev, const void* beta_dev, void* stream);
+
+/* Skinny fp16 GEMM for decode (M <= 16 rows of activations):
+ *   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n]
+ * X = A (K-contiguous rows, lda), W = B (K-contiguous rows, ldb).
+ * Requires lda, ldb multiples of 8 and 16-byte aligned A, B. */
+int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, int64_t ldb,
+                          void* C, int64_t ldc, int c_type,
+                          uint32_t M, uint32_t N, uint32_t K,
+                          float alpha, float beta, int scalar_mode,
+                          const void* alpha_dev, const void* beta_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
