@@ -147,6 +147,7 @@ def test_sgemm_strided_batched_case(handle, case):
     assert st == 0
     hGot = to_host(dC)
     # test_gemm.c compares the whole C buffer when not sampling (lines 190-195)
-    assert float(np.max(np.abs(hRef.astype(np.float64) - hGot))) < 0.1
+    if sample == 0:
+        assert float(np.max(np.abs(hRef.astype(np.float64) - hGot))) < 0.1
     rows = oracle.sample_rows(m, sample)
     _check(hRef, hGot, rows, m, n, ldc, k, offsets=[(sc * b if sc > 0 else 0) for b in range(nb)])

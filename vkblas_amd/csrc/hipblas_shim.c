@@ -187,8 +187,9 @@ static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkbla
     pthread_once(&g_real_once, real_open);
     if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return VKB_DECLINE;
     if (m > UINT32_MAX || n > UINT32_MAX || k > UINT32_MAX || batch > UINT32_MAX) return VKB_DECLINE;
-    if (lda <= 0 || ldb <= 0 || ldc <= 0 || lda > UINT32_MAX || ldb > UINT32_MAX || ldc > UINT32_MAX)
-        return VKB_DECLINE;
+    if (lda > UINT32_MAX || ldb > UINT32_MAX || ldc > UINT32_MAX) return VKB_DECLINE;
+    /* hipBLAS argument rules: the real library reports violations */
+    if (lda < (op_is_t(transA) ? k : m) || ldb < (op_is_t(transB) ? n : k) || ldc < m) return VKB_DECLINE;
     if (!alpha || !beta) return VKB_DECLINE;
 
     hipStream_t stream = NULL;
