@@ -77,6 +77,13 @@ vkblas_status_t vkblas_plan_gemm(
     uint32_t batch, uint32_t split_k, int aligned,
     vkblas_plan_t* plan);
 
+/* Process-wide kernel override for testing and tuning (the VKBLAS_TILE /
+ * VKBLAS_KERNEL environment variables set the same at load time).
+ *   tile:    -1 = planner's choice, 0 = 64x64, 1 = 128x128, 2 = 256x256
+ *   generic: 1 = always the generic blocked kernel (no pipelined variant)
+ * Returns VKBLAS_ERR_PARAM for an unknown tile. */
+vkblas_status_t vkblas_set_override(int tile, int generic);
+
 /* Path taken by the calling thread's most recent successful GEMM call. */
 int vkblas_last_path(void);
 

@@ -1,0 +1,69 @@
+"""Every GEMM kernel variant against the oracle: tile 64 / 128 / 256, the
+generic blocked kernel and the pipelined fp16 kernel, the four operand
+layouts, fp32 and fp16 inputs with fp16 and fp32 outputs, full tiles and
+ragged edges, alpha / beta.  Kernels are forced with vkblas_set_override."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(512, 768, 384), (256, 256, 128), (300, 520, 200), (96, 160, 72)]
+VARIANTS = [(tile, generic) for tile in (0, 1, 2) for generic in (False, True) if not (generic and tile != 2)]
+
+
+def rng(seed, n):
+    return np.random.default_rng(seed).uniform(-1.0, 1.0, n).astype(np.float32)
+
+
+@pytest.fixture(autouse=True)
+def reset_override():
+    import vkblas_amd as vk
+    yield
+    vk.set_override(-1, False)
+
+
+@pytest.mark.parametrize("tile,generic", VARIANTS, ids=[f"tile{64 << t}{'-generic' if g else ''}" for t, g in VARIANTS])
+@pytest.mark.parametrize("dt", ["f32", "f16>f16", "f16>f32"])
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("shape", SHAPES, ids=[f"{m}x{n}x{k}" for m, n, k in SHAPES])
+def test_kernel_variant(tile, generic, dt, op_a, op_b, shape):
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, f32_bound, F16_BOUND
+    M, N, K = shape
+    print(f"[case] tile={64 << tile} generic={generic} {dt} op={op_a}{op_b} {M}x{N}x{K}", flush=True)
+    vk.set_override(tile, generic)
+    lda = M if op_a else K
+    ldb = K if op_b else N
+    ldc = N
+    a = rng(M + N + K, lda * (K if op_a else M))
+    b = rng(M + 2 * N, ldb * (N if op_b else K))
+    c = rng(M + 3 * K, ldc * M)
+    alpha, beta = 0.75, -0.5
+    if dt == "f32":
+        ref = c.copy()
+        oracle.ref_gemm_f32_rm(op_a, op_b, M, N, K, a, lda, b, ldb, alpha, beta, ref, ldc)
+        dA, dB, dC = to_dev(a), to_dev(b), to_dev(c)
+        vk.gemm_async(vk.DT_F32, vk.DT_F32, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb,
+                      beta, dC.data_ptr(), ldc, split_k=1)
+        assert normwise(to_host(dC), ref) <= f32_bound(K)
+        return
+    ha, hb = oracle.f2h_rne(a), oracle.f2h_rne(b)
+    dA, dB = to_dev(ha), to_dev(hb)
+    if dt == "f16>f16":
+        hc = oracle.f2h_rne(c)
+        ref = hc.copy()
+        oracle.ref_gemm_f16_rm(op_a, op_b, M, N, K, ha, lda, hb, ldb, alpha, beta, ref, ldc)
+        dC = to_dev(hc)
+        vk.gemm_async(vk.DT_F16, vk.DT_F16, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb,
+                      beta, dC.data_ptr(), ldc, split_k=1)
+        assert normwise(oracle.h2f(to_host(dC)), oracle.h2f(ref)) <= F16_BOUND
+    else:
+        ref = c.copy()
+        oracle.ref_gemm_f16f32_rm(op_a, op_b, M, N, K, ha, lda, hb, ldb, alpha, beta, ref, ldc)
+        dC = to_dev(c)
+        vk.gemm_async(vk.DT_F16, vk.DT_F32, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb,
+                      beta, dC.data_ptr(), ldc, split_k=1)
+        assert normwise(to_host(dC), ref) <= F16_BOUND

@@ -78,6 +78,8 @@ def load():
                                    ctypes.POINTER(Plan)]
     L.vkblas_plan_gemm.restype = _int
     L.vkblas_last_path.restype = _int
+    L.vkblas_set_override.argtypes = [_int, _int]
+    L.vkblas_set_override.restype = _int
     L.vkblas_version.restype = ctypes.c_char_p
     L.vkblas_cache_invalidate_base.argtypes = [_vp]
     L.vkblas_cache_invalidate_base.restype = None
@@ -96,6 +98,13 @@ def plan(ab_type, c_type, op_a, op_b, M, N, K, lda, ldb, ldc, batch=1, split_k=0
     if st != OK:
         raise VkblasError(st, "vkblas_plan_gemm")
     return p
+
+
+def set_override(tile: int = -1, generic: bool = False) -> None:
+    """Force a tile (-1 planner, 0: 64, 1: 128, 2: 256) / the generic kernel."""
+    st = load().vkblas_set_override(tile, 1 if generic else 0)
+    if st != OK:
+        raise VkblasError(st, "vkblas_set_override")
 
 
 def last_path() -> int:

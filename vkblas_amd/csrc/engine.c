@@ -36,6 +36,7 @@ static int g_trace = 0;         /* VKBLAS_TRACE */
 static int g_force_tile = -1;   /* VKBLAS_TILE = 64 | 128 | 256 */
 static uint32_t g_force_split = 0; /* VKBLAS_SPLITK = n (applies when split_k == 0) */
 static int g_no_skinny = 0;     /* VKBLAS_NO_SKINNY = 1 */
+static int g_generic_only = 0;  /* VKBLAS_KERNEL = generic */
 
 static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
 static hipMemPool_t g_pool[VKB_MAX_DEVICES];
@@ -54,6 +55,7 @@ static void init_once(void) {
         g_force_split = v > 0 ? (uint32_t)v : 0;
     }
     g_no_skinny = (e = getenv("VKBLAS_NO_SKINNY")) != NULL && e[0] == '1';
+    g_generic_only = (e = getenv("VKBLAS_KERNEL")) != NULL && strcmp(e, "generic") == 0;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
     g_ndev = n;
@@ -248,6 +250,7 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         a.alpha = alpha; a.beta = beta;
         a.scalar_mode = (int)scalar_mode;
         a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
+        a.generic_only = g_generic_only;
         if (plan.path == VKBLAS_PATH_SPLITK) {
             hipMemPool_t pool = pool_for_current_device();
             if (!pool) return VKBLAS_ERR_INIT;
@@ -282,6 +285,14 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
 }
 
 int vkblas_last_path(void) { return g_last_path; }
+
+vkblas_status_t vkblas_set_override(int tile, int generic) {
+    pthread_once(&g_once, init_once);
+    if (tile < -1 || tile >= VKB_TILE_COUNT) return VKBLAS_ERR_PARAM;
+    __atomic_store_n(&g_force_tile, tile, __ATOMIC_RELAXED);
+    __atomic_store_n(&g_generic_only, generic ? 1 : 0, __ATOMIC_RELAXED);
+    return VKBLAS_OK;
+}
 
 const char* vkblas_version(void) { return VKBLAS_VERSION_STRING; }
 

@@ -52,6 +52,8 @@ typedef struct vkb_gemm_args {
     int scalar_mode;
     const void* alpha_dev;
     const void* beta_dev;
+    /* 0: best kernel for the shape; 1: always the generic blocked kernel */
+    int generic_only;
 } vkb_gemm_args;
 
 /* Tile-config properties the dispatcher plans with. */
