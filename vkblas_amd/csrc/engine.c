@@ -134,7 +134,8 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
 
     /* decode-shaped fp16: X[M<=16, K] . W[N, K]^T, both K-contiguous */
     if (ab_type == VKBLAS_DT_F16 && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 16 &&
-        batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && !g_no_skinny) {
+        batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && lda >= K && ldb >= K &&
+        !g_no_skinny) {
         plan->path = VKBLAS_PATH_SKINNY;
         plan->tile = VKB_TILE_64;
         plan->split = 1;

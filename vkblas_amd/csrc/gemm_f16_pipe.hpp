@@ -205,8 +205,9 @@ __global__ __launch_bounds__(256, 1) void gemm_f16_pipe_kernel(KParams p) {
     constexpr bool STAGED = !AK || !BKM;
 
     // Region between two barriers, stage S = K step kt:
-    //   sub-step 3 of K step kt-1 (buf 1)  + reads of (kt, sub-step 0) -> buf 0
-    //   sub-step 0 of kt (buf 0)           + reads of sub-step 1 -> buf 1, DMA of kt+1
+    //   sub-step 3 of K step kt-1 (buf 1)  + reads of (kt, sub-step 0) -> buf 0,
+    //                                        DMA of kt+1 -> stage S^1
+    //   sub-step 0 of kt (buf 0)           + reads of sub-step 1 -> buf 1
     //   sub-step 1 of kt (buf 1)           + reads of sub-step 2 -> buf 0,
     //                                        staged rows of kt+1 -> LDS stage S^1
     //   sub-step 2 of kt (buf 0)           + reads of sub-step 3 -> buf 1,
@@ -215,11 +216,17 @@ __global__ __launch_bounds__(256, 1) void gemm_f16_pipe_kernel(KParams p) {
     // Every unit (MFMA pair + its companions) is fenced with sched_barrier
     // so the compiler keeps this order and both fragment sets live.
     auto region = [&](int kt, int S, bool prev, bool next, bool next2) {
+        // The DMA of step kt+1 starts right after the barrier: stage S^1 was
+        // last read before it, and the loads get four sub-steps to land.
         if (prev) {
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 mfma_pair(1, q);
                 read_one(0, S, 0, q);
+                if (next) {
+                    dma_one(kt, S, 2 * q);
+                    dma_one(kt, S, 2 * q + 1);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -227,7 +234,7 @@ __global__ __launch_bounds__(256, 1) void gemm_f16_pipe_kernel(KParams p) {
         for (int q = 0; q < 8; ++q) {
             mfma_pair(0, q);
             read_one(1, S, 1, q);
-            if (next) {
+            if (next && !prev) {
                 dma_one(kt, S, 2 * q);
                 dma_one(kt, S, 2 * q + 1);
             }

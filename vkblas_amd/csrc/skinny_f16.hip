@@ -12,12 +12,19 @@
 //
 // Work decomposition: a workgroup owns R tiles of 16 weight rows; its WAVES
 // waves split K into contiguous slices.  Per 128-wide K step a lane streams
-// 64 contiguous bytes of one weight row (four 16-byte loads) and the matching
-// 64 bytes of one activation row, and feeds four v_mfma_f32_16x16x32_f16 per
-// row tile (src A = 16 weight rows, src B = up to 16 activation rows; unused
-// activation rows are zero).  Lane group g = lane/16 owns k in
-// [128 c + 32 g, 128 c + 32 g + 32); MFMA j of the step takes the j-th 8 of
-// those, the same k for both operands, so every k is used exactly once.
+// four 16-byte pieces of one weight row and of one activation row, and feeds
+// four v_mfma_f32_16x16x32_f16 per row tile (src A = 16 weight rows, src B =
+// up to 16 activation rows).  Lane group g = lane/16 of load / MFMA j takes k
+// in [128 c + 32 j + 8 g, +8): the same k for both operands, every k exactly
+// once, and each load instruction reads 64 contiguous bytes of each of its 16
+// rows.
+//
+// Streaming: each wave keeps D K steps of loads in flight (a rolling register
+// window; the loop is unrolled by D so window slots are static).  Loads are
+// buffer loads: the per-lane row offset is a VGPR fixed for the whole loop,
+// k goes in the scalar offset, and rows past N / activation rows past M fall
+// outside the buffer's range and read as zero.
+//
 // The waves' 16x16 partial tiles are summed in LDS in wave order (fixed
 // order: deterministic), then alpha / beta are applied once.
 #include <hip/hip_runtime.h>
@@ -51,7 +58,7 @@ __device__ __forceinline__ u32x4 ld8_checked(const _Float16* p, int nvalid) {
     return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-template <typename TC, int R, int WAVES>
+template <typename TC, int R, int WAVES, int D>
 __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
     __shared__ float red[WAVES][R][4][64];
     const int tid = threadIdx.x;
@@ -64,65 +71,98 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
     const int per = (nsteps + WAVES - 1) / WAVES;
     const int c_beg = wave * per;
     const int c_end = min(nsteps, c_beg + per);
+    const int c_full_end = max(c_beg, min(c_end, full_steps));
 
-    const bool xok = l16 < (int)p.M;
-    const _Float16* xp = p.X + (int64_t)(xok ? l16 : 0) * p.lda + g * 32;
-    const _Float16* wp[R];
-    bool wok[R];
+    // buffers on this workgroup's first weight row / the activations; the
+    // record counts make rows >= N and activation rows >= M read as zero
+    const int rows_here = min(16 * R, (int)p.N - n0);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)((int64_t)rows_here * p.ldb * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc((void*)p.X, (short)0, (int)((int64_t)p.M * p.lda * 2), 0x00020000);
+    int w_off[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int row = n0 + r * 16 + l16;
-        wok[r] = row < (int)p.N;
-        wp[r] = p.W + (int64_t)(wok[r] ? row : 0) * p.ldb + g * 32;
-    }
+    for (int r = 0; r < R; ++r) w_off[r] = (int)(((int64_t)(r * 16 + l16) * p.ldb + g * 8) * 2);
+    const int x_off = (int)(((int64_t)l16 * p.lda + g * 8) * 2);
 
     floatx4 acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
-    int c = c_beg;
-    const int c_full_end = min(c_end, full_steps);
-    // main loop: two 128-wide K steps per iteration, all loads issued first
-    for (; c + 2 <= c_full_end; c += 2) {
-        u32x4 xv[2][4], wv[2][R][4];
+    u32x4 wv[D][R][4], xv[D][4];
+    auto load_step = [&](int slot, int c) {
+        const int kb = c * 256;   // bytes
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int64_t kb = (int64_t)(c + u) * 128;
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wv[slot][r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[r] + j * 64, kb, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xv[slot][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, x_off + j * 64, kb, 0);
+    };
+    auto mma_step = [&](int slot) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < R; ++r)
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wv[slot][r][j]),
+                                                               __builtin_bit_cast(half8_t, xv[slot][j]), acc[r], 0, 0, 0);
+    };
+
+    // full K steps [c_beg, c_full_end): rolling window of D steps.  Each
+    // workgroup walks its slice starting at a rotated step, so at any moment
+    // the workgroups read different activation lines (every workgroup uses
+    // the same activations; without the rotation they all hit the same L2
+    // lines at once).  The order is fixed per workgroup: deterministic.
+    const int nfull = c_full_end - c_beg;
+    const int rot = nfull > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)nfull) : 0;
+    auto step_of = [&](int i) {   // i-th step visited, i in [0, nfull)
+        const int q = i + rot;
+        return c_beg + (q >= nfull ? q - nfull : q);
+    };
+    int i = 0;
+    if (nfull >= D) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    wv[u][r][j] = wok[r] ? *(const u32x4*)(wp[r] + kb + j * 8) : zero;
+        for (int s = 0; s < D; ++s) load_step(s, step_of(s));
+        for (; i + 2 * D <= nfull; i += D) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xv[u][j] = xok ? *(const u32x4*)(xp + kb + j * 8) : zero;
+            for (int s = 0; s < D; ++s) {
+                mma_step(s);
+                load_step(s, step_of(i + D + s));
+            }
         }
+        // drain: the last D loaded steps, then whatever is left (< D)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < R; ++r)
-                    acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                        __builtin_bit_cast(half8_t, wv[u][r][j]), __builtin_bit_cast(half8_t, xv[u][j]), acc[r], 0, 0, 0);
+        for (int s = 0; s < D; ++s) mma_step(s);
+        i += D;
     }
-    // remaining steps, including a partial last step (zero-filled beyond K)
+    for (; i < nfull; ++i) {
+        load_step(0, step_of(i));
+        mma_step(0);
+    }
+    int c = c_full_end;
+    // partial last K step (zero-filled beyond K), plain loads
+    const bool xok = l16 < (int)p.M;
     for (; c < c_end; ++c) {
         const int kb = c * 128;
-        u32x4 xv[4], wv[R][4];
+        u32x4 xt[4], wt[R][4];
+        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int nvalid = (int)p.K - (kb + g * 32 + j * 8);
+            const int k = kb + j * 32 + g * 8;
+            const int nvalid = (int)p.K - k;
 #pragma unroll
-            for (int r = 0; r < R; ++r) wv[r][j] = wok[r] ? ld8_checked(wp[r] + kb + j * 8, nvalid) : zero;
-            xv[j] = xok ? ld8_checked(xp + kb + j * 8, nvalid) : zero;
+            for (int r = 0; r < R; ++r) {
+                const int row = n0 + r * 16 + l16;
+                wt[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
+            }
+            xt[j] = xok ? ld8_checked(p.X + (int64_t)l16 * p.lda + k, nvalid) : zero;
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                    __builtin_bit_cast(half8_t, wv[r][j]), __builtin_bit_cast(half8_t, xv[j]), acc[r], 0, 0, 0);
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wt[r][j]),
+                                                               __builtin_bit_cast(half8_t, xt[j]), acc[r], 0, 0, 0);
     }
 
 #pragma unroll
@@ -157,10 +197,10 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
     }
 }
 
-template <typename TC, int R, int WAVES>
+template <typename TC, int R, int WAVES, int D>
 int launch_sk(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
-    hipLaunchKernelGGL((skinny_f16_kernel<TC, R, WAVES>), dim3(grid), dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((skinny_f16_kernel<TC, R, WAVES, D>), dim3(grid), dim3(WAVES * 64), 0, st, p);
     return (int)hipGetLastError();
 }
 
@@ -173,6 +213,9 @@ extern "C" int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, 
                                      const void* alpha_dev, const void* beta_dev, void* stream) {
     if (M == 0 || M > 16 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
     if ((lda & 7) || (ldb & 7) || ((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
+    // buffer offsets are 32-bit: a 32-row weight tile and the activations
+    // must span less than 2 GiB
+    if ((uint64_t)32 * ldb * 2 >= (1ull << 31) || (uint64_t)M * lda * 2 >= (1ull << 31)) return (int)hipErrorInvalidValue;
     SkParams p;
     p.X = (const _Float16*)X; p.W = (const _Float16*)W; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
@@ -180,9 +223,11 @@ extern "C" int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, 
     p.alpha = alpha; p.beta = beta; p.mode = scalar_mode;
     p.alpha_dev = alpha_dev; p.beta_dev = beta_dev;
     hipStream_t st = (hipStream_t)stream;
-    // 2 row tiles per workgroup while that still leaves >= 256 workgroups
-    const bool two = (N + 31) / 32 >= 256;
-    if (c_type == VKB_T_F32)
-        return two ? launch_sk<float, 2, 4>(p, st) : launch_sk<float, 1, 4>(p, st);
-    return two ? launch_sk<_Float16, 2, 4>(p, st) : launch_sk<_Float16, 1, 4>(p, st);
+    // Four waves split K with four steps in flight.  One 16-row tile per
+    // workgroup maximises workgroups; with more than 4 activation rows, two
+    // tiles share each activation load when that still leaves >= 256
+    // workgroups (one per CU).
+    const bool two = M > 4 && (N + 31) / 32 >= 256;
+    if (c_type == VKB_T_F32) return two ? launch_sk<float, 2, 4, 4>(p, st) : launch_sk<float, 1, 4, 4>(p, st);
+    return two ? launch_sk<_Float16, 2, 4, 4>(p, st) : launch_sk<_Float16, 1, 4, 4>(p, st);
 }
