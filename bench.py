@@ -29,6 +29,13 @@ PEAK_FP32_TFLOPS = 157.3     # MI355X dense fp32 matrix
 PEAK_FP16_TFLOPS = 2516.6    # MI355X dense fp16 MFMA (no sparsity)
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 
+# HBM bytes per launch of the fp32 4096^3 256x256 GEMM kernel: rocprofv3
+# FETCH_SIZE and WRITE_SIZE passes over this benchmark (KiB per dispatch,
+# averaged over the four variants), scaled by what the same counters read
+# for a 256 MiB device copy (FETCH x2.00, WRITE x1.00).  Summaries:
+# profiles/gemm_skinny_bench_traffic.txt, profiles/copy_256MiB_traffic_calibration.txt.
+TRAFFIC_F32_4096_BYTES = int((2.00 * 196754.5 + 1.00 * 66466.4) * 1024)
+
 METRIC = "TFLOPS 4096³ fp32/fp16 GEMM (% MFMA peak); fp16 matvec GB/s (% HBM peak)"
 
 
@@ -184,7 +191,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["fp32", "fp16", "matvec", "splitk", "batched"], default=None)
+    ap.add_argument("--only", choices=["fp32", "fp16", "matvec", "splitk", "batched", "calibrate"], default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -209,6 +216,13 @@ def main():
     if args.only == "batched":
         print(json.dumps(batched(torch, vk, stream, args.steps)))
         return
+    if args.only == "calibrate":
+        print(json.dumps(calibrate(torch, stream)))
+        return
+    if args.only == "fp32":
+        h = fp32_headline(torch, vk, stream, args.steps, args.warmup)
+        print(json.dumps(h))
+        return
 
     log("[bench] fp32 4096^3 x 4 variants")
     h = fp32_headline(torch, vk, stream, args.steps, args.warmup)
@@ -232,7 +246,9 @@ def main():
                    "M": 4096, "N": 4096, "K": 4096, "variants": ["NN", "NT", "TN", "TT"],
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": TRAFFIC_F32_4096_BYTES,
+                     "traffic_note": "HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated); "
+                                     "algorithmic A+B+C = 201326592 B",
                      "kernel": f"gemm_kernel<float,float,*,*,256,256,false> ({h['path']})",
                      "algorithmic": "2*4096^3 FLOP per launch"},
         "tflops_by_variant": h["tflops_by_variant"],
@@ -245,6 +261,23 @@ def main():
     log("[bench] fp16 matvec 8192x8192")
     line["fp16_matvec_8192"] = matvec(torch, vk, stream, args.steps)
     print(json.dumps(line), flush=True)
+
+
+def calibrate(torch, stream, mib=256, reps=5):
+    """A plain device copy of known size (torch's copy kernel), so that
+    rocprofv3's FETCH_SIZE / WRITE_SIZE can be scaled to bytes."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    ts = []
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        dst.copy_(src)
+        e.record(stream)
+        torch.cuda.synchronize()
+        ts.append(s.elapsed_time(e))
+    return {"copy_bytes_read": n, "copy_bytes_written": n, "ms": sorted(ts)[len(ts) // 2]}
 
 
 def splitk(torch, vk, stream, steps):
