@@ -17,11 +17,12 @@
  *   - beta == 0 never reads C (NaN/Inf already in C do not propagate).
  *   - M, N, K or batch == 0 returns VKBLAS_ERR_PARAM.
  *
+ *   - Work runs on the HIP null stream and the call returns once C is
+ *     written, as the reference's calls return after their Vulkan queue
+ *     drains.  The asynchronous, stream-aware entry points are in
+ *     vkblas_ext.h.
+ *
  * Differences from the reference, all in the caller's favour:
- *   - Work is launched asynchronously on the HIP null stream (the reference
- *     blocked on a Vulkan queue).  Callers that then hipMemcpy() the result,
- *     as the reference tests do, observe identical behaviour.  The
- *     stream-aware entry points are in vkblas_ext.h.
  *   - Every transpose variant is computed natively; there is no hidden
  *     transposed copy and no dma-buf import cache.
  *   - fp16 accepts any ldc / N parity (the reference needed even ldc and N

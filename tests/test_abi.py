@@ -18,7 +18,10 @@ def declared_functions(header):
     text = open(os.path.join(INCLUDE, header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w]*\s*\**\s+\**\s*([A-Za-z_]\w*)\s*\(", text, flags=re.M))
-    names = {n for n in names if n.startswith(("vkblas_", "hipblas"))}
+    # rocblas.h defines function-like macros of its GEMM names, so those
+    # declarations parenthesise the name: rocblas_status(rocblas_gemm_ex)(...)
+    names |= set(re.findall(r"^\s*[A-Za-z_]\w*\s*\(\s*(rocblas_\w+)\s*\)\s*\(", text, flags=re.M))
+    names = {n for n in names if n.startswith(("vkblas_", "hipblas", "rocblas_"))}
     for decl, s, d, c, z in re.findall(r"^VKBLAS_FOUR\((\w+),\s*(\w+),\s*(\w+),\s*(\w+),\s*(\w+)\)", text, flags=re.M):
         for base in (s, d, c, z):
             names.add("hipblas" + base)
@@ -38,7 +41,7 @@ def test_library_loads():
     assert L is vk.load()
 
 
-@pytest.mark.parametrize("header", ["vkblas.h", "vkblas_ext.h", "vkblas_hipblas.h"])
+@pytest.mark.parametrize("header", ["vkblas.h", "vkblas_ext.h", "vkblas_hipblas.h", "vkblas_rocblas.h"])
 def test_exports_every_declared_symbol(header):
     names = declared_functions(header)
     assert len(names) > 3, names
@@ -53,7 +56,8 @@ def test_reference_export_set_present():
             "vkblas_gemm_f16", "vkblas_gemm_f32", "hipblasGemmEx", "hipblasGemmStridedBatchedEx_v2",
             "hipblasGemmEx_v2", "hipblasSetStream", "hipblasGetStream", "hipblasSetPointerMode",
             "hipblasGetPointerMode", "hipblasSetWorkspace", "vkblas_cache_invalidate_base",
-            "hipblasHgemm", "hipblasHgemmStridedBatched", "hipblasGemmStridedBatchedEx"}
+            "hipblasHgemm", "hipblasHgemmStridedBatched", "hipblasGemmStridedBatchedEx",
+            "rocblas_gemm_ex", "rocblas_gemm_strided_batched_ex"}
     assert not (want - exported_symbols())
 
 
@@ -66,7 +70,7 @@ def test_no_cuda_or_oracle_dependency():
     out = subprocess.run(["readelf", "-d", vk.LIB_PATH], check=True, capture_output=True, text=True).stdout
     needed = re.findall(r"\[(.*?)\]", "\n".join(l for l in out.splitlines() if "NEEDED" in l))
     assert any(n.startswith("libamdhip64") for n in needed)
-    assert not any("oracle" in n or "cuda" in n or "hipblas" in n for n in needed), needed
+    assert not any("oracle" in n or "cuda" in n or "hipblas" in n or "rocblas" in n for n in needed), needed
 
 
 # --------------------------------------------------------------- planning
@@ -147,3 +151,22 @@ def test_plan_split_heuristic_and_off():
     # split count clamps so no slice is empty
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 64, 64, 100, 100, 64, 64, split_k=64)
     assert pl.split * pl.k_per_split >= 100 > (pl.split - 1) * pl.k_per_split
+
+
+def test_preload_env_puts_torch_runtime_first():
+    """The preload list leads with torch's own HIP runtime, then this library
+    (two HIP runtimes in one process would not share streams)."""
+    import os
+    from vkblas_amd import preload, LIB_PATH
+    env = preload.preload_env(base={"LD_PRELOAD": "/x/other.so"})
+    libs = env["LD_PRELOAD"].split(":")
+    rt = preload.torch_hip_runtime()
+    if rt:
+        assert libs[0] == rt and os.path.basename(rt) == "libamdhip64.so"
+        assert libs[1] == LIB_PATH
+    else:
+        assert libs[0] == LIB_PATH
+    assert libs[-1] == "/x/other.so"
+    assert preload.main([]) == 2
+    assert preload.torch_hipblas_command(["python3", "s.py", "-x"]) == ["python3", "-m", "vkblas_amd.torch_hipblas",
+                                                                         "s.py", "-x"]

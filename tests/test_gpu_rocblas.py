@@ -1,0 +1,198 @@
+"""The rocBLAS layer of libvkblas_hipblas.so: rocblas_gemm_ex and
+rocblas_gemm_strided_batched_ex (reference src/vkblas_hipblas.c:802-955), the
+calls PyTorch's hipBLAS backend makes for fp16 GEMMs.
+
+A rocBLAS handle from the real librocblas (the one the process already loaded
+with torch) drives this library's entry points through ctypes.  The oracle is
+the fp16 / fp32 CPU restatement: a column-major rocBLAS call D = alpha op(A)
+op(B) + beta C is the row-major engine call (op_a = transB, op_b = transA,
+M = n, N = m, A = b, B = a), the mapping of src/vkblas_hipblas.c:187-189.
+Bars: fp32 normwise <= 1e-5 sqrt(K), fp16 normwise <= 2e-3.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+OP = {0: 111, 1: 112}            # rocblas_operation none / transpose
+F16, F32, BF16 = 150, 151, 168   # rocblas_datatype
+HOST, DEVICE = 0, 1              # rocblas_pointer_mode
+
+_vp, _i, _i64, _u32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32
+
+
+class RocblasHandle:
+    def __init__(self):
+        import torch  # noqa: F401  (loads the process's librocblas)
+        import vkblas_amd as vk
+        self.lib = vk.load()
+        self.real = ctypes.CDLL("librocblas.so.5")
+        self.h = _vp()
+        assert self.real.rocblas_create_handle(ctypes.byref(self.h)) == 0
+        L = self.lib
+        L.rocblas_gemm_ex.restype = _i
+        L.rocblas_gemm_ex.argtypes = [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _vp, _i, _i,
+                                      _vp, _i, _i, _i, _i, ctypes.c_int32, _u32]
+        L.rocblas_gemm_strided_batched_ex.restype = _i
+        L.rocblas_gemm_strided_batched_ex.argtypes = [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i64, _vp, _i, _i,
+                                                      _i64, _vp, _vp, _i, _i, _i64, _vp, _i, _i, _i64, _i, _i, _i,
+                                                      ctypes.c_int32, _u32]
+
+    def set_stream(self, s):
+        assert self.real.rocblas_set_stream(self.h, _vp(s)) == 0
+
+    def set_pointer_mode(self, mode):
+        assert self.real.rocblas_set_pointer_mode(self.h, mode) == 0
+
+    def close(self):
+        self.real.rocblas_destroy_handle(self.h)
+
+
+@pytest.fixture(scope="module")
+def rh():
+    import torch
+    h = RocblasHandle()
+    h.set_stream(torch.cuda.current_stream().cuda_stream)
+    yield h
+    h.close()
+
+
+def _rng_f16(seed, n, scale=1.0):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal(n) * scale).astype(np.float16).view(np.uint16)
+
+
+def _expected(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, ctype):
+    """column-major rocBLAS semantics via the row-major engine oracle"""
+    out = C.copy()
+    if ctype == F16:
+        oracle.ref_gemm_f16_rm(tb, ta, n, m, k, B, ldb, A, lda, alpha, beta, out, ldc)
+    else:
+        oracle.ref_gemm_f16f32_rm(tb, ta, n, m, k, B, ldb, A, lda, alpha, beta, out, ldc)
+    return out
+
+
+def _cols(buf, m, n, ld):
+    return np.concatenate([buf[j * ld: j * ld + m] for j in range(n)])
+
+
+CASES = [(ta, tb, m, n, k, alpha, beta, ct)
+         for (m, n, k) in ((64, 48, 40), (257, 129, 65), (256, 256, 256), (8, 4096, 512))
+         for ta in (0, 1) for tb in (0, 1)
+         for (alpha, beta) in ((1.0, 0.0), (0.5, -0.25))
+         for ct in (F16, F32)]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"{'NT'[c[0]]}{'NT'[c[1]]}_{c[2]}x{c[3]}x{c[4]}_a{c[5]}_b{c[6]}_"
+                                                     f"{'f16' if c[7] == F16 else 'f32'}")
+def test_gemm_ex_f16(rh, case):
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, fbox
+    ta, tb, m, n, k, alpha, beta, ct = case
+    print(f"[case] rocblas_gemm_ex f16 {case}", flush=True)
+    lda = (k if ta else m) + 1
+    ldb = (n if tb else k) + 2
+    ldc = m + 3
+    A = _rng_f16(1, lda * (m if ta else k), 1 / np.sqrt(k))
+    B = _rng_f16(2, ldb * (k if tb else n))
+    C = _rng_f16(3, ldc * n) if ct == F16 else np.random.default_rng(3).standard_normal(ldc * n).astype(np.float32)
+    want = _expected(ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, ct)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[ta], OP[tb], m, n, k, fbox(alpha), dA.data_ptr(), F16, lda, dB.data_ptr(),
+                                F16, ldb, fbox(beta), dC.data_ptr(), ct, ldc, dC.data_ptr(), ct, ldc, F32, 0, 0, 0)
+    assert st == 0
+    got = to_host(dC)
+    if ct == F16:
+        assert normwise(oracle.h2f(_cols(got, m, n, ldc)), oracle.h2f(_cols(want, m, n, ldc))) <= F16_BOUND
+    else:
+        assert normwise(_cols(got, m, n, ldc), _cols(want, m, n, ldc)) <= F16_BOUND
+    pad = np.ones(got.size, bool)
+    for j in range(n):
+        pad[j * ldc: j * ldc + m] = False
+    assert np.array_equal(got[pad], C[pad])   # rows m..ldc-1 of each column untouched
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 1), (0, 1), (1, 0)])
+def test_gemm_ex_f32(rh, ta, tb):
+    from gpu_helpers import to_dev, to_host, normwise, f32_bound, fbox
+    m, n, k = 300, 200, 150
+    print(f"[case] rocblas_gemm_ex f32 {ta}{tb}", flush=True)
+    lda, ldb, ldc = (k if ta else m), (n if tb else k), m
+    A, B, C = oracle.fill_test_gemm(5 + 2 * ta + tb, lda * (m if ta else k), ldb * (k if tb else n), ldc * n)
+    want = C.copy()
+    oracle.ref_gemm_cm(ta, tb, m, n, k, 0.5, A, lda, B, ldb, 0.7, want, ldc)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[ta], OP[tb], m, n, k, fbox(0.5), dA.data_ptr(), F32, lda, dB.data_ptr(),
+                                F32, ldb, fbox(0.7), dC.data_ptr(), F32, ldc, dC.data_ptr(), F32, ldc, F32, 0, 0, 0)
+    assert st == 0
+    assert normwise(to_host(dC), want) <= f32_bound(k)
+
+
+def test_separate_d_and_device_scalars(rh):
+    """D != C (C copied into D first), scalars in device memory."""
+    import torch
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND
+    m, n, k = 130, 70, 96
+    print("[case] rocblas_gemm_ex separate D, device pointer mode", flush=True)
+    A = _rng_f16(11, m * k, 1 / np.sqrt(k))
+    B = _rng_f16(12, k * n)
+    C = _rng_f16(13, m * n)
+    want = _expected(0, 0, m, n, k, 2.0, A, m, B, k, 0.5, C, m, F16)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    dD = torch.full((m * n,), float("nan"), dtype=torch.float16, device="cuda:0")
+    scal = torch.tensor([2.0, 0.5], dtype=torch.float32, device="cuda:0")
+    rh.set_pointer_mode(DEVICE)
+    try:
+        st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], m, n, k, scal.data_ptr(), dA.data_ptr(), F16, m,
+                                    dB.data_ptr(), F16, k, scal.data_ptr() + 4, dC.data_ptr(), F16, m, dD.data_ptr(),
+                                    F16, m, F32, 0, 0, 0)
+    finally:
+        rh.set_pointer_mode(HOST)
+    assert st == 0
+    assert normwise(oracle.h2f(to_host(dD)), oracle.h2f(want)) <= F16_BOUND
+    assert np.array_equal(to_host(dC), C)   # C is read-only
+
+
+def test_strided_batched_f16(rh):
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, fbox
+    m, n, k, nb = 96, 80, 64, 3
+    print("[case] rocblas_gemm_strided_batched_ex f16", flush=True)
+    sa, sb, sc = m * k + 7, k * n + 5, m * n + 3
+    A = _rng_f16(21, sa * nb, 1 / np.sqrt(k))
+    B = _rng_f16(22, sb * nb)
+    C = _rng_f16(23, sc * nb)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    st = rh.lib.rocblas_gemm_strided_batched_ex(rh.h, OP[1], OP[0], m, n, k, fbox(1.0), dA.data_ptr(), F16, k, sa,
+                                                dB.data_ptr(), F16, k, sb, fbox(1.0), dC.data_ptr(), F16, m, sc,
+                                                dC.data_ptr(), F16, m, sc, nb, F32, 0, 0, 0)
+    assert st == 0
+    got = to_host(dC)
+    for i in range(nb):
+        want = _expected(1, 0, m, n, k, 1.0, A[i * sa:], k, B[i * sb:], k, 1.0, C[i * sc: i * sc + m * n].copy(), m,
+                         F16)
+        assert normwise(oracle.h2f(got[i * sc: i * sc + m * n]), oracle.h2f(want)) <= F16_BOUND
+
+
+def test_forwarded_calls_still_work(rh):
+    """bf16 (no kernels here) and m == 0 (quick return) reach the real rocBLAS."""
+    import torch
+    from gpu_helpers import fbox
+    print("[case] rocblas_gemm_ex forwarded bf16 / m=0", flush=True)
+    m = n = k = 64
+    a = torch.randn(m, k, device="cuda:0").bfloat16()
+    b = torch.randn(k, n, device="cuda:0").bfloat16()
+    c = torch.zeros(n, m, device="cuda:0").bfloat16()
+    # column-major: A^T as stored (k x m col-major = a row-major), C = a @ b in row-major = (b^T a^T)^T
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], n, m, k, fbox(1.0), b.data_ptr(), BF16, n, a.data_ptr(), BF16,
+                                k, fbox(0.0), c.data_ptr(), BF16, n, c.data_ptr(), BF16, n, F32, 0, 0, 0)
+    assert st == 0
+    torch.cuda.synchronize()
+    ref = a.float().cpu() @ b.float().cpu()
+    got = c.float().cpu().reshape(m, n)
+    assert float((got - ref).abs().max() / ref.abs().max()) < 2e-2
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], 0, n, k, fbox(1.0), b.data_ptr(), F16, n, a.data_ptr(), F16,
+                                k, fbox(0.0), c.data_ptr(), F16, n, c.data_ptr(), F16, n, F32, 0, 0, 0)
+    assert st == 0

@@ -299,22 +299,29 @@ const char* vkblas_version(void) { return VKBLAS_VERSION_STRING; }
 
 /* ------------------------------------------------------ reference C API */
 
+/* The reference's engine calls return once C is written (src/vkblas.c:963
+ * waits for its queue); these do the same on the null stream they launch on. */
+static vkblas_status_t finish_sync(vkblas_status_t st) {
+    if (st == VKBLAS_OK && hipStreamSynchronize(NULL) != hipSuccess) return VKBLAS_ERR_INIT;
+    return st;
+}
+
 vkblas_status_t vkblas_gemm_f32(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
                                 float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
                                 float beta, void* C, uint32_t ldc, uint32_t batch,
                                 int64_t stride_a, int64_t stride_b, int64_t stride_c) {
-    return vkblas_gemm_async(VKBLAS_DT_F32, VKBLAS_DT_F32, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta,
-                             C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL, NULL, 0,
-                             NULL);
+    return finish_sync(vkblas_gemm_async(VKBLAS_DT_F32, VKBLAS_DT_F32, op_a, op_b, M, N, K, alpha, A, lda, B, ldb,
+                                         beta, C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL,
+                                         NULL, 0, NULL));
 }
 
 vkblas_status_t vkblas_gemm_f16(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
                                 float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
                                 float beta, void* C, uint32_t ldc, uint32_t batch,
                                 int64_t stride_a, int64_t stride_b, int64_t stride_c) {
-    return vkblas_gemm_async(VKBLAS_DT_F16, VKBLAS_DT_F16, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta,
-                             C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL, NULL, 0,
-                             NULL);
+    return finish_sync(vkblas_gemm_async(VKBLAS_DT_F16, VKBLAS_DT_F16, op_a, op_b, M, N, K, alpha, A, lda, B, ldb,
+                                         beta, C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST, NULL,
+                                         NULL, 0, NULL));
 }
 
 vkblas_status_t vkblas_gemm_bf16(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K,
