@@ -341,22 +341,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
         } else {
             // v_mfma_f32_32x32x2_f32: lane holds 1 k of one row.  Lane half h
             // owns k in [16 h, 16 h + 16) of the 32-wide step, one per MFMA.
+            // Fragments are double-buffered: the reads of chunk q+1 are issued
+            // before the 4 TM TN MFMAs of chunk q, so LDS latency stays hidden.
+            // Each read is fenced (sched_barrier) between groups of MFMAs so the
+            // compiler cannot sink it next to its first use.
+            constexpr int NF = TM + TN;                 // fragment reads per chunk
+            constexpr int NM = 4 * TM * TN;             // MFMAs per chunk
+            u32x4 af[2][TM], bf[2][TN];
+            auto read_frag = [&](int q, int buf, int f) {
+                const int c = h * 4 + q;
+                if (f < TN) bf[buf][f] = Bs[brow[f] * 8 + swz(brow[f], c)];
+                else af[buf][f - TN] = As[arow[f - TN] * 8 + swz(arow[f - TN], c)];
+            };
+#pragma unroll
+            for (int f = 0; f < NF; ++f) read_frag(0, 0, f);
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int c = h * 4 + q;
-                u32x4 af[TM], bf[TN];
 #pragma unroll
-                for (int j = 0; j < TN; ++j) bf[j] = Bs[brow[j] * 8 + swz(brow[j], c)];
-#pragma unroll
-                for (int i = 0; i < TM; ++i) af[i] = As[arow[i] * 8 + swz(arow[i], c)];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-#pragma unroll
-                    for (int i = 0; i < TM; ++i)
-#pragma unroll
-                        for (int j = 0; j < TN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                __uint_as_float(bf[j][e]), __uint_as_float(af[i][e]), acc[i][j], 0, 0, 0);
+                for (int u = 0; u < NM; ++u) {
+                    const int e = u / (TM * TN), i = (u / TN) % TM, j = u % TN;
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bf[q & 1][j][e]),
+                                                                    __uint_as_float(af[q & 1][i][e]), acc[i][j],
+                                                                    0, 0, 0);
+                    if (q < 3 && u % (NM / NF) == 0) read_frag(q + 1, (q + 1) & 1, u / (NM / NF));
+                    if (u % (NM / NF) == NM / NF - 1) __builtin_amdgcn_sched_barrier(0);
+                }
             }
         }
         if (more) {
