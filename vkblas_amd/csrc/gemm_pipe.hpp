@@ -8,11 +8,14 @@
 // dispatched from src/vkblas.c:1191-1313, 1822-1868).
 //
 // Per workgroup: 4 waves, 2x2, each owning a 128x128 block of C held in 256
-// AGPRs as 4x4 32x32 MFMA accumulators.  A K step is 128 bytes of K (64 fp16
-// or 32 fp32) and four sub-steps of one 16-byte chunk per lane half:
-//  * fp16: sub-step s = v_mfma_f32_32x32x16_f16 over chunk 2s + h, 16 MFMAs;
-//  * fp32: sub-step s = v_mfma_f32_32x32x2_f32 over chunk 4h + s, one MFMA per
-//    k of the chunk, 64 MFMAs.
+// AGPRs.  A K step is 128 bytes of K (64 fp16 or 32 fp32):
+//  * fp16, both operands K-major: two sub-steps of v_mfma_f32_16x16x32_f16
+//    on 8x8 16x16 tiles (64 MFMAs each; lane group g = lane / 16 takes chunk
+//    4s + g);
+//  * fp16 with an MN-major operand: four sub-steps of
+//    v_mfma_f32_32x32x16_f16 on 4x4 32x32 tiles (chunk 2s + h, 16 MFMAs);
+//  * fp32: four sub-steps of v_mfma_f32_32x32x2_f32 on 4x4 32x32 tiles (one
+//    MFMA per k of chunk 4h + s, 64 MFMAs each).
 // Per K step:
 //  * K-major operand tiles go global -> LDS directly (buffer_load ... lds:
 //    lane l of a wave writes 16 B at M0 + 16 l), so they use no VGPRs and no
@@ -43,7 +46,7 @@
 //    moves odd groups to the other half of the bank line, which separates
 //    rows r and r + 8 that share r & 7.
 // Every row base has its low three bits clear, so a fragment's slot index is
-// (base + (hoff ^ g)) ^ sub-step offset (2s for fp16, s for fp32).
+// (base + (hoff ^ g)) ^ sub-step offset (4s, 2s or s by MFMA shape).
 //
 // Global traffic uses buffer loads on resources based at the tile's first
 // element: a fixed per-lane VGPR offset plus a uniform SGPR offset (row step
@@ -160,50 +163,109 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     };
     constexpr bool STAGED = !AK || !BKM;
 
-    // fragment slot bases: row base + (hoff ^ g(row)); sub-step s reads
-    // base ^ (s * SX)
-    constexpr int SX = F16 ? 2 : 1;
-    const int hoff = F16 ? h : 4 * h;
-    auto frag_base = [&](int r, bool kmajor) {
-        return kmajor ? (r >> 3) * GRP + (r & 7) * 8 + (hoff ^ (r & 7)) : r * 8 + (hoff ^ ((r ^ (r >> 3)) & 7));
-    };
-    int xa[4], xb[4];
+    // ---- MFMA shape --------------------------------------------------------
+    // SH 0, fp16 with both operands K-major: v_mfma_f32_16x16x32_f16; a
+    //   sub-step is one 32-wide k slice (chunks 4s + g, lane group
+    //   g = lane / 16 holds 8 k of row lane % 16); the wave's 128x128 block is
+    //   8x8 tiles of 16x16 (floatx4).  With random data gfx950 sustains ~15%
+    //   more fp16 FLOP/s on 16x16x32 than on 32x32x16 (half the accumulator
+    //   traffic per FLOP under the power limit).
+    // SH 1, fp16 with a staged (MN-major) operand: v_mfma_f32_32x32x16_f16,
+    //   sub-step s = chunk 2s + h, 4x4 tiles of 32x32 (floatx16); the staged
+    //   registers leave no room for the 16x16 shape's fragment sets.
+    // SH 2, fp32: v_mfma_f32_32x32x2_f32, sub-step s = chunk 4h + s (one MFMA
+    //   per k), 4x4 tiles of 32x32.
+    constexpr int SH = F16 ? ((AK && BKM) ? 0 : 1) : 2;
+    constexpr int NSUB = SH == 0 ? 2 : 4;           // sub-steps per K step
+    constexpr int UPS = 32 / NSUB;                  // units per sub-step
+    constexpr int NF = SH == 0 ? 8 : 4;             // fragments per operand
+    constexpr int FR = SH == 0 ? 16 : 32;           // rows per fragment
+    constexpr int SX = SH == 0 ? 4 : (SH == 1 ? 2 : 1);   // sub-step slot offset
+    const int fl = SH == 0 ? (lane & 15) : l32;     // fragment row of this lane
+    const int hoff = SH == 0 ? (lane >> 4) : (SH == 1 ? h : 4 * h);   // chunk in sub-step 0
+
+    // Fragment slot of row r: row base + (hoff ^ g(r)); sub-step s reads it
+    // ^ (s * SX).  Fragment i starts FR rows further on (FR = 16 or 32, a
+    // multiple of 8): its row base moves by the constant ROWSTEP, and g moves
+    // by d(i) = 0 for K-major tiles (g = r & 7) and by ((FR / 8) i) & 7 for
+    // MN-major tiles (g = (r ^ (r >> 3)) & 7: the lane's (r >> 3) & 7 is
+    // fl >> 3 < FR / 8, so adding (FR / 8) i carries into no bit it uses and
+    // acts as an XOR).  The address of fragment i in sub-step s is therefore
+    // base[d(i) ^ s SX] + i ROWSTEP, and i ROWSTEP goes in the ds_read
+    // immediate offset.
+    auto row_base = [&](int r, bool kmajor) { return kmajor ? (r >> 3) * GRP + (r & 7) * 8 : r * 8; };
+    auto gsw = [&](int r, bool kmajor) { return kmajor ? (r & 7) : ((r ^ (r >> 3)) & 7); };
+    constexpr int ASTEP = AK ? (FR / 8) * GRP : FR * 8;
+    constexpr int BSTEP = BKM ? (FR / 8) * GRP : FR * 8;
+    auto dsw = [](bool kmajor, int i) { return kmajor ? 0 : ((FR / 8) * i) & 7; };
+    int xa[8], xb[8];   // indexed by the slot XOR; unused entries are dead code
+    {
+        const int ra = wm * 128 + fl, rb = wn * 128 + fl;
+        const int a0 = row_base(ra, AK), ag = hoff ^ gsw(ra, AK);
+        const int b0 = row_base(rb, BKM), bg = hoff ^ gsw(rb, BKM);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        xa[i] = frag_base(wm * 128 + i * 32 + l32, AK);
-        xb[i] = frag_base(wn * 128 + i * 32 + l32, BKM);
+        for (int c = 0; c < 8; ++c) {
+            xa[c] = A0 + a0 + (ag ^ c);
+            xb[c] = B0 + b0 + (bg ^ c);
+        }
     }
 
-    floatx16 acc[4][4];
+    using acc_t = std::conditional_t<SH == 0, floatx4, floatx16>;
+    constexpr int AR = SH == 0 ? 4 : 16;            // accumulator registers per tile
+    acc_t acc[NF][NF];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NF; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NF; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < AR; ++r) acc[i][j][r] = 0.0f;
 
-    u32x4 af[2][4], bf[2][4];
-    // A sub-step is 8 units (one fragment read of the next sub-step each).
-    // fp16: unit q = MFMAs of tiles (q/2, 2(q%2)) and (q/2, 2(q%2)+1), so the
-    //   next sub-step's fragments are read in the order B0 B1 A0 B2 B3 A1 A2 A3.
-    // fp32: unit q = k element q/2 of the chunk on the 8 tiles of half q%2
-    //   (rows i = 2(q%2), 2(q%2)+1), reads in the order B0..B3 A0..A3.
+    // A sub-step is UPS units; each unit also reads one fragment of the next
+    // sub-step, in the order the next sub-step first uses them.
+    // SH 0: unit q = tiles (q/2, 4(q%2) .. +3): reads B0-B3 A0 B4-B7 A1 .. A7.
+    //   A_i is last used by unit 2i+1 and its successor is read in a later
+    //   unit (A0 at 4, A_i at 8+i), so A needs one register set; B needs two.
+    // SH 1: unit q = tiles (q/2, 2(q%2) .. +1): reads B0 B1 A0 B2 B3 A1 A2 A3.
+    // SH 2: unit q = k element q/2 of the chunk on tiles (2(q%2) .. +1, 0..3):
+    //   reads B0..B3 A0..A3.
+    // SH 1 and 2 keep every fragment to the sub-step's end: two sets each.
+    constexpr int NAB = SH == 0 ? 1 : 2;
+    u32x4 af[NAB][NF], bf[2][NF];
     auto read_one = [&](int buf, int S, int s, int idx) {
-        constexpr int isA16[8] = {0, 0, 1, 0, 0, 1, 1, 1};
-        constexpr int fi16[8] = {0, 1, 0, 2, 3, 1, 2, 3};
-        const bool isA = F16 ? isA16[idx] : idx >= 4;
-        const int fi = F16 ? fi16[idx] : (idx & 3);
-        if (isA) af[buf][fi] = lds[A0 + S * STG + (xa[fi] ^ (SX * s))];
-        else bf[buf][fi] = lds[B0 + S * STG + (xb[fi] ^ (SX * s))];
+        bool isA;
+        int fi;
+        if constexpr (SH == 0) {
+            constexpr int isA16[16] = {0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1};
+            constexpr int fi16[16] = {0, 1, 2, 3, 0, 4, 5, 6, 7, 1, 2, 3, 4, 5, 6, 7};
+            isA = isA16[idx];
+            fi = fi16[idx];
+        } else if constexpr (SH == 1) {
+            constexpr int isA8[8] = {0, 0, 1, 0, 0, 1, 1, 1};
+            constexpr int fi8[8] = {0, 1, 0, 2, 3, 1, 2, 3};
+            isA = isA8[idx];
+            fi = fi8[idx];
+        } else {
+            isA = idx >= 4;
+            fi = idx & 3;
+        }
+        if (isA) af[buf % NAB][fi] = lds[xa[dsw(AK, fi) ^ (SX * s)] + S * STG + fi * ASTEP];
+        else bf[buf][fi] = lds[xb[dsw(BKM, fi) ^ (SX * s)] + S * STG + fi * BSTEP];
     };
     auto mfma_unit = [&](int buf, int q) {
-        if constexpr (F16) {
-            const int i = q >> 1, j = (q & 1) * 2;
+        if constexpr (SH == 0) {
+            const int i = q >> 1, j0 = (q & 1) * 4;
 #pragma unroll
-            for (int jj = j; jj < j + 2; ++jj)
-                acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bf[buf][jj]),
-                                                                    __builtin_bit_cast(half8_t, af[buf][i]),
-                                                                    acc[i][jj], 0, 0, 0);
+            for (int j = j0; j < j0 + 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, bf[buf][j]),
+                                                                  __builtin_bit_cast(half8_t, af[buf % NAB][i]),
+                                                                  acc[i][j], 0, 0, 0);
+        } else if constexpr (SH == 1) {
+            const int i = q >> 1, j0 = (q & 1) * 2;
+#pragma unroll
+            for (int j = j0; j < j0 + 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bf[buf][j]),
+                                                                  __builtin_bit_cast(half8_t, af[buf % NAB][i]),
+                                                                  acc[i][j], 0, 0, 0);
         } else {
             const int e = q >> 1, i0 = (q & 1) * 2;
 #pragma unroll
@@ -211,67 +273,50 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bf[buf][j][e]),
-                                                                    __uint_as_float(af[buf][i][e]), acc[i][j], 0, 0, 0);
+                                                                    __uint_as_float(af[buf % NAB][i][e]), acc[i][j],
+                                                                    0, 0, 0);
         }
     };
 
-    // The 16 DMA loads of a K step are spread over DMA_UNITS consecutive
-    // units from the region's first: issued in a burst they oversubscribe the
-    // texture address unit and stall the MFMA issue.
+    // A region (between two barriers) is 32 units: the last sub-step of K step
+    // kt-1 (units [0, UPS), from registers) and the first NSUB-1 sub-steps of
+    // kt.  The 16 DMA loads of kt+1 are spread over DMA_UNITS units from the
+    // first (issued in a burst they oversubscribe the texture address unit
+    // and stall the MFMA issue); staged MN-major rows of kt+1 are written in
+    // units [16, 24) and the staged loads of kt+2 issued in [24, 32), after
+    // every DMA, which the end-of-region wait relies on.  The first region
+    // has no previous sub-step: its units start at UPS and its DMA is spread
+    // over [UPS, 24).
     constexpr int DMA_UNITS = VKB_PIPE_DMA_UNITS;
-    // the first region's DMA starts at unit 8 and must end before the staged
-    // loads of unit 24 (the end-of-region wait counts on that order)
-    static_assert(DMA_UNITS >= 1 && DMA_UNITS <= 16, "DMA must precede the staged loads");
-    auto dma_unit = [&](int kt, int S, int v) {   // v: unit index from the first
+    static_assert(DMA_UNITS >= 1 && DMA_UNITS <= 24, "the DMA must precede the staged loads of unit 24");
+    auto dma_unit = [&](int kt, int S, int u, bool prev) {   // u: unit of the region
+        const int first = prev ? 0 : UPS;
+        const int span = prev ? DMA_UNITS : 24 - UPS;
+        const int v = u - first;
 #pragma unroll
         for (int n = 0; n < 16; ++n)
-            if (n * DMA_UNITS >= v * 16 && n * DMA_UNITS < (v + 1) * 16) dma_load(kt, S, n);
+            if (n * span >= v * 16 && n * span < (v + 1) * 16) dma_load(kt, S, n);
     };
 
-    // Region between two barriers, stage S = K step kt:
-    //   sub-step 3 of K step kt-1 (buf 1)  + reads of (kt, sub-step 0) -> buf 0
-    //   sub-step 0 of kt (buf 0)           + reads of sub-step 1 -> buf 1
-    //   sub-step 1 of kt (buf 1)           + reads of sub-step 2 -> buf 0,
-    //                                        staged rows of kt+1 -> LDS stage S^1
-    //   sub-step 2 of kt (buf 0)           + reads of sub-step 3 -> buf 1,
-    //                                        staged loads of kt+2 -> VGPRs
-    //   the DMA of kt+1 -> stage S^1 spread over the first DMA_UNITS units
+    // Region, stage S = K step kt:
+    //   sub-step NSUB-1 of K step kt-1 (its buffer)  + reads of (kt, 0)
+    //   sub-steps 0 .. NSUB-2 of kt                  + reads of the next one
+    //   DMA of kt+1 -> stage S^1; staged rows / loads (see above)
     //   wait for this wave's DMA and LDS traffic, barrier
+    // Sub-step s of K step kt uses fragment buffer s & 1 (NSUB is even).
     // Every unit (MFMAs + companions) is fenced with sched_barrier so the
     // compiler keeps this order and both fragment sets live.
     auto region = [&](int kt, int S, bool prev, bool next, bool next2) {
-        // stage S^1 was last read before the barrier that opened this region
-        const int u0 = prev ? 0 : 8;   // first unit of this region
-        if (prev) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                mfma_unit(1, q);
-                read_one(0, S, 0, q);
-                if (next) dma_unit(kt + 1, S ^ 1, q - u0);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            mfma_unit(0, q);
-            read_one(1, S, 1, q);
-            if (next) dma_unit(kt + 1, S ^ 1, 8 + q - u0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            mfma_unit(1, q);
-            read_one(0, S, 2, q);
-            if (next) dma_unit(kt + 1, S ^ 1, 16 + q - u0);
-            if (STAGED && next) stage_store(S ^ 1, q);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            mfma_unit(0, q);
-            read_one(1, S, 3, q);
-            if (next) dma_unit(kt + 1, S ^ 1, 24 + q - u0);
-            if (STAGED && next2) stage_load(kt + 2, q);
+        for (int u = prev ? 0 : UPS; u < 32; ++u) {
+            const int sub = u / UPS - 1;          // sub-step of kt run here (-1: kt-1's last)
+            const int q = u % UPS;
+            const int buf = sub < 0 ? (NSUB - 1) & 1 : sub & 1;
+            mfma_unit(buf, q);
+            read_one((sub + 1) & 1, S, sub + 1, q);
+            if (next) dma_unit(kt + 1, S ^ 1, u, prev);
+            if (STAGED && next && u >= 16 && u < 24) stage_store(S ^ 1, u - 16);
+            if (STAGED && next2 && u >= 24) stage_load(kt + 2, u - 24);
             __builtin_amdgcn_sched_barrier(0);
         }
         // DMA of kt+1 landed (staged loads of kt+2 may still fly)
@@ -295,7 +340,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     }
     sync_vm(std::integral_constant<int, NSTAGED>{});
 #pragma unroll
-    for (int q = 0; q < 8; ++q) read_one(0, 0, 0, q);
+    for (int q = 0; q < UPS; ++q) read_one(0, 0, 0, q);
 
     // nkt is even: regions alternate stages 0 and 1; the loop body is
     // branch-free, the last two regions load less
@@ -314,20 +359,23 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
         region(kt + 2, 1, true, false, false);
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) mfma_unit(1, q);   // sub-step 3 of the last K step
+    for (int q = 0; q < UPS; ++q) mfma_unit((NSUB - 1) & 1, q);   // last sub-step of the last K step
 
     // ---- epilogue: C[m][n..n+3] = alpha * acc + beta * C ----
+    // 16x16 tiles: lane holds n = 4 (lane / 16) + e of row m = lane % 16;
+    // 32x32 tiles: register 4 q + e holds n = 8 q + 4 h + e of row m = l32.
     float alpha, beta;
     load_scalars(p, alpha, beta);
+    constexpr int NQ = SH == 0 ? 1 : 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + wm * 128 + i * 32 + l32;
+    for (int i = 0; i < NF; ++i) {
+        const int m = m0 + wm * 128 + i * FR + fl;
         TC* crow = Cb + (int64_t)m * p.ldc;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NF; ++j) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = n0 + wn * 128 + j * 32 + q * 8 + h * 4;
+            for (int q = 0; q < NQ; ++q) {
+                const int n = n0 + wn * 128 + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
                 float x[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e];
