@@ -361,31 +361,74 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 #pragma unroll
     for (int q = 0; q < UPS; ++q) mfma_unit((NSUB - 1) & 1, q);   // last sub-step of the last K step
 
-    // ---- epilogue: C[m][n..n+3] = alpha * acc + beta * C ----
+    // ---- epilogue: C = alpha * acc (+ beta * C) ----
     // 16x16 tiles: lane holds n = 4 (lane / 16) + e of row m = lane % 16;
     // 32x32 tiles: register 4 q + e holds n = 8 q + 4 h + e of row m = l32.
     float alpha, beta;
     load_scalars(p, alpha, beta);
     constexpr int NQ = SH == 0 ? 1 : 4;
+    const float beta_u = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, beta)));
+    if (beta_u == 0.0f) {
+        // Staged through LDS so C leaves as whole rows: the MFMA layout
+        // spreads a store instruction over 16-32 rows of C, the texture
+        // address unit then handles a line per row.  Each wave owns an LDS
+        // region (the K loop's last barrier has retired every tile read) with
+        // rows padded by 16 bytes: the MFMA-layout writes then fall on
+        // distinct banks and each 16-lane row read covers all 64.  fp32
+        // (512-byte rows) goes in two passes of 64 rows.
+        constexpr int ROWB = 128 * (int)sizeof(TC);          // bytes of a wave-block row
+        constexpr int STR = ROWB + 16;                       // padded LDS row stride
+        constexpr int PASSES = sizeof(TC) == 4 ? 2 : 1;
+        constexpr int PROWS = 128 / PASSES;                  // rows per pass
+        constexpr int LPR = ROWB / 16;                       // lanes per row on read-out
+        static_assert(4 * PROWS * STR <= 9216 * 16, "epilogue staging exceeds LDS");
+        char* wl = (char*)lds + wave * (PROWS * STR);
+        TC* cblk = Cb + (int64_t)(m0 + wm * 128) * p.ldc + (n0 + wn * 128);
 #pragma unroll
-    for (int i = 0; i < NF; ++i) {
-        const int m = m0 + wm * 128 + i * FR + fl;
-        TC* crow = Cb + (int64_t)m * p.ldc;
+        for (int pass = 0; pass < PASSES; ++pass) {
 #pragma unroll
-        for (int j = 0; j < NF; ++j) {
+            for (int i = 0; i < NF; ++i) {
+                const int m = i * FR + fl - pass * PROWS;   // row within this pass
+                if (i * FR < pass * PROWS || i * FR >= (pass + 1) * PROWS) continue;
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-                const int n = n0 + wn * 128 + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
-                float x[4];
+                for (int j = 0; j < NF; ++j) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e];
-                if (beta != 0.0f) {
-                    float o[4];
+                    for (int q = 0; q < NQ; ++q) {
+                        const int n = j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
+                        float x[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e];
+                        store4<TC>((TC*)(wl + m * STR + n * (int)sizeof(TC)), x, true);
+                    }
+                }
+            }
+            // a wave's LDS operations complete in order; the wait keeps the
+            // compiler from reordering the cross-lane read-back
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int it = 0; it < PROWS * LPR / 64; ++it) {
+                const int r = it * (64 / LPR) + lane / LPR, c = lane % LPR;
+                const u32x4 v = *(const u32x4*)(wl + r * STR + c * 16);
+                *(u32x4*)((char*)(cblk + (int64_t)(pass * PROWS + r) * p.ldc) + c * 16) = v;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            const int m = m0 + wm * 128 + i * FR + fl;
+            TC* crow = Cb + (int64_t)m * p.ldc;
+#pragma unroll
+            for (int j = 0; j < NF; ++j) {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    const int n = n0 + wn * 128 + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
+                    float x[4], o[4];
                     load4<TC>(crow + n, o, true);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] += beta * o[e];
+                    for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e] + beta * o[e];
+                    store4<TC>(crow + n, x, true);
                 }
-                store4<TC>(crow + n, x, true);
             }
         }
     }
