@@ -1,0 +1,114 @@
+"""Edge cases of the decode kernels (engine op_a = N, op_b = T, M <= 16: the
+GEMV kernel for M <= 4, the MFMA skinny kernel above), the path the
+reference reaches for matvec / skinny shapes (src/vkblas.c:2100-2392,
+2501-2808).  Ragged K (not a multiple of the kernels' K steps), padded
+leading dimensions whose padding holds NaN (it must never reach C), beta != 0,
+fp32 output and device-memory scalars; the oracle is the fp16 CPU
+restatement.  Bar: normwise <= 2e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+NAN16 = np.uint16(0x7E00)
+
+CASES = []
+for M in (1, 2, 3, 4, 5, 8, 16):
+    for (N, K) in ((1, 8), (7, 504), (100, 520), (1000, 1032), (300, 4104), (64, 8192)):
+        CASES.append((M, N, K, 0, 0, 0.0, "f16"))
+CASES += [
+    (1, 1000, 1032, 8, 16, 0.0, "f16"),
+    (3, 333, 4104, 24, 8, -0.5, "f16"),
+    (4, 1024, 2048, 0, 0, 0.25, "f32"),
+    (8, 777, 1000, 16, 8, -0.5, "f16"),
+    (16, 512, 520, 8, 0, 1.0, "f32"),
+    (2, 4096, 4096, 0, 0, 0.0, "f32"),
+]
+
+
+def _padded(rows, cols, ld, seed, scale):
+    """rows x cols fp16 matrix in a buffer of (rows-1)*ld + cols elements,
+    NaN in the padding between rows."""
+    r = np.random.default_rng(seed)
+    buf = np.full((rows - 1) * ld + cols, NAN16, np.uint16)
+    vals = oracle.f2h_rne((r.standard_normal(rows * cols) * scale).astype(np.float32))
+    for i in range(rows):
+        buf[i * ld: i * ld + cols] = vals[i * cols:(i + 1) * cols]
+    return buf
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"M{c[0]}_N{c[1]}_K{c[2]}_pa{c[3]}_pb{c[4]}_b{c[5]}_{c[6]}")
+def test_decode_edges(case):
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND
+    M, N, K, pad_a, pad_b, beta, out = case
+    print(f"[case] decode edge {case}", flush=True)
+    lda, ldb, ldc = K + pad_a, K + pad_b, N
+    hX = _padded(M, K, lda, 1 + M + K, 1.0)
+    hW = _padded(N, K, ldb, 2 + N + K, 0.05)
+    f16 = out == "f16"
+    r = np.random.default_rng(3)
+    if f16:
+        hC = oracle.f2h_rne(r.standard_normal(M * ldc).astype(np.float32))
+    else:
+        hC = r.standard_normal(M * ldc).astype(np.float32)
+    want = hC.copy()
+    if f16:
+        oracle.ref_gemm_f16_rm(0, 1, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
+    else:
+        oracle.ref_gemm_f16f32_rm(0, 1, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
+    dX, dW, dC = to_dev(hX), to_dev(hW), to_dev(hC)
+    vk.gemm_async(vk.DT_F16, vk.DT_F16 if f16 else vk.DT_F32, vk.OP_N, vk.OP_T, M, N, K, 1.5, dX.data_ptr(), lda,
+                  dW.data_ptr(), ldb, beta, dC.data_ptr(), ldc, stream=torch.cuda.current_stream().cuda_stream)
+    assert vk.last_path() == vk.PATH_SKINNY
+    got = to_host(dC)
+    if f16:
+        g, w = oracle.h2f(got), oracle.h2f(want)
+    else:
+        g, w = got, want
+    assert np.all(np.isfinite(g))
+    assert normwise(g, w) <= F16_BOUND
+
+
+@pytest.mark.parametrize("M", [1, 4, 12])
+def test_decode_device_scalars(M):
+    """alpha / beta in device memory (hipBLAS pointer mode device)."""
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND
+    N, K = 640, 1536
+    print(f"[case] decode device scalars M={M}", flush=True)
+    hX = _padded(M, K, K, 11, 1.0)
+    hW = _padded(N, K, K, 12, 0.05)
+    hC = oracle.f2h_rne(np.random.default_rng(13).standard_normal(M * N).astype(np.float32))
+    want = hC.copy()
+    oracle.ref_gemm_f16_rm(0, 1, M, N, K, hX, K, hW, K, 0.75, 0.5, want, N)
+    dX, dW, dC = to_dev(hX), to_dev(hW), to_dev(hC)
+    sc = torch.tensor([0.75, 0.5], dtype=torch.float32, device="cuda:0")
+    vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_T, M, N, K, 0.0, dX.data_ptr(), K, dW.data_ptr(), K, 0.0,
+                  dC.data_ptr(), N, scalar_mode=vk.SCALAR_DEV_F32, alpha_dev=sc.data_ptr(),
+                  beta_dev=sc.data_ptr() + 4, stream=torch.cuda.current_stream().cuda_stream)
+    assert vk.last_path() == vk.PATH_SKINNY
+    assert normwise(oracle.h2f(to_host(dC)), oracle.h2f(want)) <= F16_BOUND
+
+
+def test_decode_deterministic():
+    """The decode kernels sum in a fixed order: repeated runs are bitwise equal."""
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host
+    print("[case] decode determinism", flush=True)
+    for M in (1, 3, 9):
+        N, K = 2048, 4096
+        dX, dW = to_dev(_padded(M, K, K, 21, 1.0)), to_dev(_padded(N, K, K, 22, 0.05))
+        outs = []
+        for _ in range(3):
+            dC = torch.empty(M * N, dtype=torch.float16, device="cuda:0")
+            vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_T, M, N, K, 1.0, dX.data_ptr(), K, dW.data_ptr(), K,
+                          0.0, dC.data_ptr(), N, stream=torch.cuda.current_stream().cuda_stream)
+            outs.append(to_host(dC))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])

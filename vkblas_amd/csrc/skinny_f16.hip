@@ -34,6 +34,7 @@
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -74,12 +75,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
     const int c_full_end = max(c_beg, min(c_end, full_steps));
 
     // buffers on this workgroup's first weight row / the activations; the
-    // record counts make rows >= N and activation rows >= M read as zero
+    // record counts are the read domains ((rows - 1) ld + K elements), so
+    // rows >= N and activation rows >= M read as zero
     const int rows_here = min(16 * R, (int)p.N - n0);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)((int64_t)rows_here * p.ldb * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rx =
-        __builtin_amdgcn_make_buffer_rsrc((void*)p.X, (short)0, (int)((int64_t)p.M * p.lda * 2), 0x00020000);
+        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)(((int64_t)(rows_here - 1) * p.ldb + p.K) * 2),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + p.K) * 2), 0x00020000);
     int w_off[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) w_off[r] = (int)(((int64_t)(r * 16 + l16) * p.ldb + g * 8) * 2);
@@ -197,6 +200,147 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
     }
 }
 
+// ---------------------------------------------------------------- GEMV
+// For M <= 2 activation rows (token-by-token decode) the MFMA tile is mostly
+// idle and its fragment layout splits every load over 16 rows (half lines).
+// Here a wave reads 1 KB of ONE weight row per instruction (8 whole 128-byte
+// lines, loaded non-temporal: the weights stream through once, and whole-line
+// requests let nt skip the cache without re-fetching the other half of a
+// line): lane l takes k in [c*512 + 8 l, +8) of chunk c and multiplies it
+// with the same k of each activation row (v_dot2_f32_f16, fp32 accumulate).
+// Workgroup: 4 waves, RB weight rows; wave w takes chunks w, w+4, ... of K,
+// loading the next chunk's RB rows while it computes the current one.
+// Partials (MM x RB per lane) are summed across the 64 lanes by a butterfly
+// reduce-scatter, then across the 4 waves in wave order: deterministic.
+template <typename TC, int MM, int RB>
+__global__ __launch_bounds__(256) void gemv_f16_kernel(SkParams p) {
+    constexpr int P = MM * RB;                    // partials per lane (power of 2, <= 64)
+    constexpr int LP = P == 2 ? 1 : P == 4 ? 2 : P == 8 ? 3 : P == 16 ? 4 : P == 32 ? 5 : 6;
+    static_assert((1 << LP) == P, "MM * RB must be a power of 2 in [2, 64]");
+    __shared__ float red[4][P];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * RB;
+    const int rows_here = min(RB, (int)p.N - n0);
+    // The buffer ranges are exactly the operands' read domains ((rows - 1) ld
+    // + K elements): rows past N, activation rows past M and k past K in the
+    // last row read as zero and never touch memory beyond the allocation.
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)(((int64_t)(rows_here - 1) * p.ldb + p.K) * 2),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + p.K) * 2), 0x00020000);
+    const int nch = (int)((p.K + 511) / 512);
+
+    float acc[MM][RB];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[m][r] = 0.0f;
+
+    u32x4 wc[RB], xc[MM];
+    auto load = [&](int c, u32x4* w, u32x4* x) {
+        const int kb = (c * 512 + lane * 8) * 2;   // byte offset within a row
+#pragma unroll
+        for (int m = 0; m < MM; ++m) x[m] = __builtin_amdgcn_raw_buffer_load_b128(rx, m * (int)p.lda * 2 + kb, 0, 0);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)   // streamed once: non-temporal (nt)
+            w[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, r * (int)p.ldb * 2 + kb, 0, 2);
+    };
+    auto compute = [&](int c, const u32x4* w, const u32x4* x) {
+        // lanes past K (last chunk) contribute nothing; the weight row's
+        // padding past K may hold anything, so both operands are zeroed
+        const bool valid = c * 512 + lane * 8 < (int)p.K;
+        const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const u32x4 wr = valid ? w[r] : z;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) {
+                const u32x4 xm = valid ? x[m] : z;
+                float a = acc[m][r];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // element copied out first: a bit cast of a vector
+                    // subscript compiled to element 0 for every e
+                    const uint32_t we = wr[e], xe = xm[e];
+                    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, we), __builtin_bit_cast(half2_t, xe), a,
+                                               false);
+                }
+                acc[m][r] = a;
+            }
+        }
+    };
+    int c = wave;
+    if (c < nch) load(c, wc, xc);
+    for (; c < nch; c += 4) {
+        u32x4 wn[RB], xn[MM];
+        const bool more = c + 4 < nch;
+        if (more) load(c + 4, wn, xn);
+        compute(c, wc, xc);
+        if (more) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r) wc[r] = wn[r];
+#pragma unroll
+            for (int m = 0; m < MM; ++m) xc[m] = xn[m];
+        }
+    }
+
+    // butterfly reduce-scatter over lane bits 0 .. LP-1, then a plain
+    // butterfly over the rest: lane l ends with the 64-lane total of
+    // partial j(l) = sum_t bit_t(l) * (P >> (t + 1)).
+    float v[P];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) v[m * RB + r] = acc[m][r];
+#pragma unroll
+    for (int t = 0; t < LP; ++t) {
+        const int H = P >> (t + 1);
+        const bool upper = (lane >> t) & 1;
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            const float send = upper ? v[i] : v[i + H];
+            const float keep = upper ? v[i + H] : v[i];
+            v[i] = keep + __shfl_xor(send, 1 << t);
+        }
+    }
+#pragma unroll
+    for (int t = LP; t < 6; ++t) v[0] += __shfl_xor(v[0], 1 << t);
+    if (lane < P) {
+        int j = 0;
+#pragma unroll
+        for (int t = 0; t < LP; ++t) j += ((lane >> t) & 1) * (P >> (t + 1));
+        red[wave][j] = v[0];
+    }
+    __syncthreads();
+
+    if (tid < P) {
+        const int m = tid / RB, r = tid % RB;
+        if (m < (int)p.M && n0 + r < (int)p.N) {
+            float alpha = p.alpha, beta = p.beta;
+            if (p.mode == 1) {
+                alpha = *(const float*)p.alpha_dev;
+                beta = *(const float*)p.beta_dev;
+            } else if (p.mode == 2) {
+                alpha = (float)*(const _Float16*)p.alpha_dev;
+                beta = (float)*(const _Float16*)p.beta_dev;
+            }
+            const float s = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+            TC* dst = (TC*)p.C + (int64_t)m * p.ldc + n0 + r;
+            float y = alpha * s;
+            if (beta != 0.0f) y += beta * (float)*dst;
+            *dst = (TC)y;
+        }
+    }
+}
+
+template <typename TC, int MM, int RB>
+int launch_gemv(const SkParams& p, hipStream_t st) {
+    const uint32_t grid = (p.N + RB - 1) / RB;
+    hipLaunchKernelGGL((gemv_f16_kernel<TC, MM, RB>), dim3(grid), dim3(256), 0, st, p);
+    return (int)hipGetLastError();
+}
+
 template <typename TC, int R, int WAVES, int D>
 int launch_sk(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
@@ -227,6 +371,13 @@ extern "C" int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, 
     // workgroup maximises workgroups; with more than 4 activation rows, two
     // tiles share each activation load when that still leaves >= 256
     // workgroups (one per CU).
+    // M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best
+    // for 4096-14336 rows); more activation rows multiply its VALU work and
+    // registers, and the MFMA kernel is faster from M = 3 on.
+    if (M <= 2) {
+        if (c_type == VKB_T_F32) return M == 1 ? launch_gemv<float, 1, 4>(p, st) : launch_gemv<float, 2, 4>(p, st);
+        return M == 1 ? launch_gemv<_Float16, 1, 4>(p, st) : launch_gemv<_Float16, 2, 4>(p, st);
+    }
     const bool two = M > 4 && (N + 31) / 32 >= 256;
     if (c_type == VKB_T_F32) return two ? launch_sk<float, 2, 4, 4>(p, st) : launch_sk<float, 1, 4, 4>(p, st);
     return two ? launch_sk<_Float16, 2, 4, 4>(p, st) : launch_sk<_Float16, 1, 4, 4>(p, st);
