@@ -34,7 +34,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 # averaged over the four variants), scaled by what the same counters read
 # for a 256 MiB device copy (FETCH x2.00, WRITE x1.00).  Summaries:
 # profiles/gemm_skinny_bench_traffic.txt, profiles/copy_256MiB_traffic_calibration.txt.
-TRAFFIC_F32_4096_BYTES = int((2.00 * 196754.5 + 1.00 * 66466.4) * 1024)
+TRAFFIC_F32_4096_BYTES = int((2.00 * 198440.0 + 1.00 * 68736.0) * 1024)
 
 METRIC = "TFLOPS 4096³ fp32/fp16 GEMM (% MFMA peak); fp16 matvec GB/s (% HBM peak)"
 
@@ -249,7 +249,7 @@ def main():
                      "frac": round(achieved / PEAK_FP32_TFLOPS, 4), "traffic": TRAFFIC_F32_4096_BYTES,
                      "traffic_note": "HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE (copy-calibrated); "
                                      "algorithmic A+B+C = 201326592 B",
-                     "kernel": f"gemm_kernel<float,float,*,*,256,256,false> ({h['path']})",
+                     "kernel": f"gemm_pipe_kernel<float,float,*,*> ({h['path']})",
                      "algorithmic": "2*4096^3 FLOP per launch"},
         "tflops_by_variant": h["tflops_by_variant"],
     }
