@@ -281,7 +281,7 @@ def calibrate(torch, stream, mib=256, reps=5):
 
 
 def splitk(torch, vk, stream, steps):
-    """M=N=256 tall-K split-K, fp32 and fp16, split {4,16,64}."""
+    """M=N=256 tall-K split-K, fp32 and fp16, split {4,16,64} and the planner's choice."""
     sp = stream.cuda_stream
     out = {}
     for K in (65536, 262144):
@@ -291,7 +291,7 @@ def splitk(torch, vk, stream, steps):
             if dt == "f16":
                 A, B = A.half(), B.half()
             C = torch.empty(256 * 256, device="cuda:0")
-            for split in (4, 16, 64):
+            for split in (4, 16, 64, 0):   # 0: the planner's choice
                 def call():
                     vk.gemm_async(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, 1.0,
                                   A.data_ptr(), K, B.data_ptr(), 256, 0.0, C.data_ptr(), 256, split_k=split,
@@ -305,7 +305,12 @@ def splitk(torch, vk, stream, steps):
                 med = ts[len(ts) // 2]
                 tf = 2.0 * 256 * 256 * K / (med * 1e-3) / 1e12
                 gbs = (A.numel() + B.numel()) * A.element_size() / (med * 1e-3) / 1e9
-                out[f"K{K}_{dt}_s{split}"] = {"ms": round(med, 4), "tflops": round(tf, 2), "GBps": round(gbs, 1)}
+                key = f"K{K}_{dt}_s{split}" if split else f"K{K}_{dt}_auto"
+                out[key] = {"ms": round(med, 4), "tflops": round(tf, 2), "GBps": round(gbs, 1)}
+                if not split:
+                    pl = vk.plan(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256)
+                    out[key]["split"] = pl.split
+                    out[key]["tile"] = 64 << pl.tile
             del A, B
     return out
 

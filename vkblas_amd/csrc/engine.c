@@ -150,14 +150,23 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         if (split_k > 1) {
             split = split_k;
         } else if (split_k == 0) {
-            /* few output tiles and a long K: split K so ~256 workgroups run */
-            uint64_t tiles = (uint64_t)cdiv(M, vkb_tile_bm(tile)) * cdiv(N, vkb_tile_bn(tile));
+            /* Few output tiles and a long K: split K.  128x128 tiles (reuse
+             * of each A / B slice over 128 columns / rows) when the output
+             * allows; slices of at least 1024 k; up to ~512 workgroups (two
+             * per CU) and 128 slices.  Measured at M = N = 256: K = 65536 ->
+             * 64 slices, K = 262144 -> 128 slices are the fastest choices. */
+            const int stile = (M >= 128 && N >= 128 && g_force_tile < 0) ? VKB_TILE_128 : tile;
+            uint64_t tiles = (uint64_t)cdiv(M, vkb_tile_bm(stile)) * cdiv(N, vkb_tile_bn(stile));
             if (tiles < 64 && K >= 4096) {
-                uint64_t want = 256 / tiles;
+                uint64_t want = K / 1024;
+                if (want > 512 / tiles) want = 512 / tiles;
+                if (want > 128) want = 128;
                 uint64_t kmax = K / (8 * bk);   /* keep >= 8 K steps per slice */
                 if (want > kmax) want = kmax;
-                if (want > 64) want = 64;
-                split = want >= 2 ? (uint32_t)want : 1;
+                if (want >= 2) {
+                    split = (uint32_t)want;
+                    tile = stile;
+                }
             }
         }
     }
