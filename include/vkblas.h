@@ -66,9 +66,10 @@ vkblas_status_t vkblas_gemm_f32(
     uint32_t batch,
     int64_t stride_a, int64_t stride_b, int64_t stride_c);
 
-/* bf16 GEMM (A, B, C bf16; fp32 accumulate).  Reference `src/vkblas.h:41-50`.
- * Not on this build's hot path yet: returns VKBLAS_ERR_INIT so callers
- * (the hipBLAS shim) forward to the vendor library. */
+/* bf16 GEMM: A, B, C bf16; products and sums in fp32 (MFMA
+ * v_mfma_f32_*_bf16); the result is rounded to bf16 once, to nearest even.
+ * Reference `src/vkblas.h:41-50` / `src/vkblas.c:3345-3446`.  Runs on the
+ * null stream and returns once C is written. */
 vkblas_status_t vkblas_gemm_bf16(
     vkblas_op_t op_a, vkblas_op_t op_b,
     uint32_t M, uint32_t N, uint32_t K,
@@ -81,7 +82,9 @@ vkblas_status_t vkblas_gemm_bf16(
     int64_t stride_a, int64_t stride_b, int64_t stride_c);
 
 /* bf16 entry used by the reference's hipBLAS translation
- * (`src/vkblas.h:55-64`).  Same status as vkblas_gemm_bf16. */
+ * (`src/vkblas.h:55-64`, `src/vkblas.c:3448-3512`).  Same contract and result
+ * as vkblas_gemm_bf16 (the reference's variant differed only in an internal
+ * transpose-avoidance choice). */
 vkblas_status_t vkblas_gemm_bf16_hipblas(
     vkblas_op_t op_a, vkblas_op_t op_b,
     uint32_t M, uint32_t N, uint32_t K,

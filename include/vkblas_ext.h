@@ -15,7 +15,7 @@
 extern "C" {
 #endif
 
-typedef enum { VKBLAS_DT_F32 = 0, VKBLAS_DT_F16 = 1 } vkblas_dtype_t;
+typedef enum { VKBLAS_DT_F32 = 0, VKBLAS_DT_F16 = 1, VKBLAS_DT_BF16 = 2 } vkblas_dtype_t;
 
 /* How alpha / beta are passed (hipBLAS pointer modes). */
 typedef enum {
@@ -44,7 +44,8 @@ typedef struct {
 /*
  * General GEMM on a caller-chosen HIP stream (NULL = null stream).
  *   ab_type: type of A and B; c_type: type of C
- *     (F32, F32) | (F16, F16) | (F16, F32).  fp32 accumulation throughout.
+ *     (F32, F32) | (F16, F16) | (F16, F32) | (BF16, BF16) | (BF16, F32).
+ *     fp32 accumulation throughout; 16-bit results rounded to nearest even.
  *   split_k: 0 = heuristic, 1 = never split, >1 = force that many K slices
  *            (clamped so every slice is non-empty).
  * Returns VKBLAS_OK, VKBLAS_ERR_PARAM (bad arguments / unsupported type

@@ -6,8 +6,10 @@
  * (ROCm 7.2); the shim includes this header next to <hipblas/hipblas.h>, so
  * the compiler checks every declaration here against the vendor's.
  *
- * Computed by this library (gfx950 kernels), forwarded to the real hipBLAS
- * when declined (degenerate sizes, other types):
+ * Computed by this library (gfx950 kernels): Sgemm*, Hgemm*, and GemmEx* with
+ * fp32 data, fp16 data (fp16 or fp32 result) and bf16 data (bf16 or fp32
+ * result).  Forwarded to the real hipBLAS when declined (degenerate sizes,
+ * other types).
  */
 #pragma once
 #include <hipblas/hipblas.h>

@@ -10,8 +10,9 @@
  * checks every declaration against the vendor's.  The names are parenthesised
  * because rocblas.h also defines function-like macros of the same names.
  *
- * Computed by this library: fp32 x fp32 -> fp32, fp16 x fp16 -> fp16 and
- * fp16 x fp16 -> fp32 with compute type f32_r; any D (D == C, or a separate D
+ * Computed by this library: fp32 x fp32 -> fp32, fp16 x fp16 -> fp16,
+ * fp16 x fp16 -> fp32, bf16 x bf16 -> bf16 and bf16 x bf16 -> fp32 with
+ * compute type f32_r; any D (D == C, or a separate D
  * that C is copied into first when beta may be nonzero).  Everything else
  * (other types, other compute types, solution queries, degenerate sizes) is
  * forwarded to the real rocBLAS of the process.

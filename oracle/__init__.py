@@ -14,7 +14,11 @@ The arithmetic lives in ``ref_gemm.c`` (built into ``liboracle.so`` by
 * ``ref_gemm_f16_rm``  -- ``test/test_h.c:63-79`` (row-major fp16, double
   accumulation, one fp16 rounding, to nearest even);
 * ``fill_test_h``      -- ``test/test_h.c:102,111-113``;
-* ``ref_gemm_f32_rm``  -- the row-major engine contract ``src/vkblas.h:21-26``.
+* ``ref_gemm_f32_rm``  -- the row-major engine contract ``src/vkblas.h:21-26``;
+* ``f2bf_rne`` / ``bf2f`` -- bf16 conversions of
+  ``src/shaders/gemm_half_128x128_bankfree_tmpl.comp:26-47``;
+* ``ref_gemm_bf16_rm`` -- ``src/vkblas.c:3345-3512`` (bf16 in, fp32
+  arithmetic, one bf16 rounding) on the row-major engine contract.
 """
 from __future__ import annotations
 
@@ -54,6 +58,8 @@ def lib():
         L.oracle_f2h_ties_away.restype = ctypes.c_uint16
         L.oracle_f2h_ties_away.argtypes = [ctypes.c_float]
         L.oracle_f2h_rne_array.argtypes = [_f32p, _u16p, _i64]
+        L.oracle_f2bf_rne_array.argtypes = [_f32p, _u16p, _i64]
+        L.oracle_bf2f_array.argtypes = [_u16p, _f32p, _i64]
         L.oracle_h2f_array.argtypes = [_u16p, _f32p, _i64]
         L.oracle_fill_test_gemm.argtypes = [ctypes.c_uint, _f32p, _i64, _f32p, _i64, _f32p, _i64]
         L.oracle_fill_test_h.argtypes = [ctypes.c_uint, _u16p, _i64, _u16p, _i64, _u16p, _i64]
@@ -67,6 +73,9 @@ def lib():
                                              _u16p, _i64, rows_t, _int, _int]
         L.oracle_ref_gemm_f16f32_rm.argtypes = [_int, _int, _int, _int, _int, _u16p, _i64, _u16p, _i64, _flt,
                                                 _flt, _f32p, _i64, rows_t, _int, _int]
+        for nm in ("oracle_ref_gemm_bf16_rm",):
+            getattr(L, nm).argtypes = L.oracle_ref_gemm_f16_rm.argtypes
+        L.oracle_ref_gemm_bf16f32_rm.argtypes = L.oracle_ref_gemm_f16f32_rm.argtypes
         L.oracle_ref_gemm_f32_rm.argtypes = [_int, _int, _int, _int, _int, _f32p, _i64, _f32p, _i64, _flt, _flt,
                                              _f32p, _i64, rows_t, _int, _int]
         _lib = L
@@ -88,6 +97,22 @@ def h2f(h) -> np.ndarray:
     h = np.ascontiguousarray(h, dtype=np.uint16)
     y = np.empty(h.shape, dtype=np.float32)
     lib().oracle_h2f_array(h.reshape(-1), y.reshape(-1), h.size)
+    return y
+
+
+def f2bf_rne(x) -> np.ndarray:
+    """float32 array -> bf16 bit patterns (uint16), round to nearest even."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f2bf_rne_array(x.reshape(-1), y.reshape(-1), x.size)
+    return y
+
+
+def bf2f(h) -> np.ndarray:
+    """bf16 bit patterns (uint16) -> float32."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_bf2f_array(h.reshape(-1), y.reshape(-1), h.size)
     return y
 
 
@@ -156,4 +181,20 @@ def ref_gemm_f32_rm(op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, B
     """fp32 engine contract (row-major, beta == 0 never reads C), in place on C."""
     p, n, keep = _rows_arg(rows)
     lib().oracle_ref_gemm_f32_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc, p, n, threads)
+    del keep
+
+
+def ref_gemm_bf16_rm(op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, B, ldb: int,
+                     alpha: float, beta: float, C, ldc: int, rows=None, threads: int = 0) -> None:
+    """bf16 GEMM (vkblas_gemm_bf16), in place on C (uint16 bf16 patterns, row-major)."""
+    p, n, keep = _rows_arg(rows)
+    lib().oracle_ref_gemm_bf16_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc, p, n, threads)
+    del keep
+
+
+def ref_gemm_bf16f32_rm(op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, B, ldb: int,
+                        alpha: float, beta: float, C, ldc: int, rows=None, threads: int = 0) -> None:
+    """bf16 inputs, fp32 result (GemmEx 16BF -> 32F), in place on C (float32, row-major)."""
+    p, n, keep = _rows_arg(rows)
+    lib().oracle_ref_gemm_bf16f32_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc, p, n, threads)
     del keep

@@ -32,6 +32,22 @@
  *                          with ties rounded away from zero, which is what the
  *                          reference's f2h computes for these finite inputs.
  *   oracle_f2h_rne / oracle_h2f  IEEE binary16 conversions.
+ *   oracle_bf2f / oracle_f2bf_rne  bfloat16 conversions as the reference's
+ *                          shaders state them: bf16 -> fp32 is the bit
+ *                          pattern shifted left 16
+ *                          (src/shaders/gemm_half_128x128_bankfree_tmpl.comp:26-40),
+ *                          fp32 -> bf16 rounds to nearest even
+ *                          (same file :41-47, src/shaders/cvt_tmpl.comp:141).
+ *                          NaN maps to a quiet NaN of the same sign; the
+ *                          reference's integer rounding can carry a NaN with
+ *                          a large payload into the sign bit, which nothing
+ *                          in its tests exercises.
+ *   oracle_ref_gemm_bf16_rm / oracle_ref_gemm_bf16f32_rm  the bf16 GEMM of
+ *                          src/vkblas.c:3345-3512 (gemm_bf16_core: bf16
+ *                          inputs, fp32 arithmetic, one bf16 rounding) on the
+ *                          row-major engine contract, with the arithmetic of
+ *                          oracle_ref_gemm_f16_rm (double accumulation of the
+ *                          exact products, then alpha * (float)s + beta * C).
  *
  * The *_omp variants split the same arithmetic over output columns with
  * OpenMP (each output is still computed by one thread in the same order).
@@ -110,6 +126,29 @@ void oracle_h2f_array(const uint16_t* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = oracle_h2f(x[i]);
 }
 
+/* ------------------------------------------------------------ bf16 bits */
+
+float oracle_bf2f(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t oracle_f2bf_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u); /* quiet NaN */
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+void oracle_f2bf_rne_array(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_f2bf_rne(x[i]);
+}
+void oracle_bf2f_array(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = oracle_bf2f(x[i]);
+}
+
 /* ------------------------------------------------------------- generators */
 
 void oracle_fill_test_gemm(unsigned seed, float* A, int64_t na, float* B, int64_t nb, float* C, int64_t nc) {
@@ -178,24 +217,58 @@ void oracle_ref_gemm_cm(int ta, int tb, int m, int n, int k, float alpha, const 
 
 /* ------------------------------------------------------ fp16 row-major */
 
-/* fp16 -> fp32 table (filled before any parallel region) */
+/* 16-bit -> fp32 tables (filled before any parallel region) */
 static float g_h2f_lut[65536];
+static float g_bf2f_lut[65536];
 static int g_h2f_ready = 0;
 static void h2f_lut_init(void) {
     if (g_h2f_ready) return;
-    for (uint32_t i = 0; i < 65536u; ++i) g_h2f_lut[i] = oracle_h2f((uint16_t)i);
+    for (uint32_t i = 0; i < 65536u; ++i) {
+        g_h2f_lut[i] = oracle_h2f((uint16_t)i);
+        g_bf2f_lut[i] = oracle_bf2f((uint16_t)i);
+    }
     g_h2f_ready = 1;
 }
 
-static double dot_f16(int op_a, int op_b, int m, int n, int K, const uint16_t* A, int64_t lda,
-                      const uint16_t* B, int64_t ldb) {
+static double dot_half(const float* lut, int op_a, int op_b, int m, int n, int K, const uint16_t* A,
+                       int64_t lda, const uint16_t* B, int64_t ldb) {
     double s = 0.0;
     for (int k = 0; k < K; ++k) {
-        float av = op_a ? g_h2f_lut[A[(int64_t)k * lda + m]] : g_h2f_lut[A[(int64_t)m * lda + k]];
-        float bv = op_b ? g_h2f_lut[B[(int64_t)n * ldb + k]] : g_h2f_lut[B[(int64_t)k * ldb + n]];
+        float av = op_a ? lut[A[(int64_t)k * lda + m]] : lut[A[(int64_t)m * lda + k]];
+        float bv = op_b ? lut[B[(int64_t)n * ldb + k]] : lut[B[(int64_t)k * ldb + n]];
         s += (double)av * bv;
     }
     return s;
+}
+
+/* Shared body of the 16-bit-input GEMMs.  bf != 0 selects bf16 inputs (and a
+ * bf16 result when C16 is given); exactly one of C16 / C32 is non-NULL. */
+static void ref_gemm_half_rm(int bf, int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
+                             const uint16_t* B, int64_t ldb, float alpha, float beta, uint16_t* C16, float* C32,
+                             int64_t ldc, const int* rows, int nrows, int threads) {
+    int nr = rows ? nrows : M;
+    h2f_lut_init();
+    const float* lut = bf ? g_bf2f_lut : g_h2f_lut;
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
+#endif
+    for (int ri = 0; ri < nr; ++ri) {
+        for (int n = 0; n < N; ++n) {
+            const int m = rows ? rows[ri] : ri;
+            const int64_t at = (int64_t)m * ldc + n;
+            double s = dot_half(lut, op_a, op_b, m, n, K, A, lda, B, ldb);
+            if (C16) {
+                float old = beta != 0.0f ? lut[C16[at]] : 0.0f;
+                float v = alpha * (float)s + beta * old;
+                C16[at] = bf ? oracle_f2bf_rne(v) : oracle_f2h_rne(v);
+            } else {
+                float old = beta != 0.0f ? C32[at] : 0.0f;
+                C32[at] = alpha * (float)s + beta * old;
+            }
+        }
+    }
+    (void)threads;
 }
 
 /* op_a / op_b: engine ops (0 = N, 1 = T); rows: optional list of the rows m
@@ -203,41 +276,25 @@ static double dot_f16(int op_a, int op_b, int m, int n, int K, const uint16_t* A
 void oracle_ref_gemm_f16_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
                             const uint16_t* B, int64_t ldb, float alpha, float beta, uint16_t* C, int64_t ldc,
                             const int* rows, int nrows, int threads) {
-    int nr = rows ? nrows : M;
-    h2f_lut_init();
-#ifdef _OPENMP
-    if (threads <= 0) threads = omp_get_max_threads();
-#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
-#endif
-    for (int ri = 0; ri < nr; ++ri) {
-        for (int n = 0; n < N; ++n) {
-            const int m = rows ? rows[ri] : ri;
-            double s = dot_f16(op_a, op_b, m, n, K, A, lda, B, ldb);
-            float old = beta != 0.0f ? oracle_h2f(C[(int64_t)m * ldc + n]) : 0.0f;
-            C[(int64_t)m * ldc + n] = oracle_f2h_rne(alpha * (float)s + beta * old);
-        }
-    }
-    (void)threads;
+    ref_gemm_half_rm(0, op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, NULL, ldc, rows, nrows, threads);
 }
 
 void oracle_ref_gemm_f16f32_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
                                const uint16_t* B, int64_t ldb, float alpha, float beta, float* C, int64_t ldc,
                                const int* rows, int nrows, int threads) {
-    int nr = rows ? nrows : M;
-    h2f_lut_init();
-#ifdef _OPENMP
-    if (threads <= 0) threads = omp_get_max_threads();
-#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
-#endif
-    for (int ri = 0; ri < nr; ++ri) {
-        for (int n = 0; n < N; ++n) {
-            const int m = rows ? rows[ri] : ri;
-            double s = dot_f16(op_a, op_b, m, n, K, A, lda, B, ldb);
-            float old = beta != 0.0f ? C[(int64_t)m * ldc + n] : 0.0f;
-            C[(int64_t)m * ldc + n] = alpha * (float)s + beta * old;
-        }
-    }
-    (void)threads;
+    ref_gemm_half_rm(0, op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, NULL, C, ldc, rows, nrows, threads);
+}
+
+void oracle_ref_gemm_bf16_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
+                             const uint16_t* B, int64_t ldb, float alpha, float beta, uint16_t* C, int64_t ldc,
+                             const int* rows, int nrows, int threads) {
+    ref_gemm_half_rm(1, op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, NULL, ldc, rows, nrows, threads);
+}
+
+void oracle_ref_gemm_bf16f32_rm(int op_a, int op_b, int M, int N, int K, const uint16_t* A, int64_t lda,
+                                const uint16_t* B, int64_t ldb, float alpha, float beta, float* C, int64_t ldc,
+                                const int* rows, int nrows, int threads) {
+    ref_gemm_half_rm(1, op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, NULL, C, ldc, rows, nrows, threads);
 }
 
 /* fp32 row-major engine contract (src/vkblas.h:21-26), same arithmetic as

@@ -7,7 +7,8 @@ with torch) drives this library's entry points through ctypes.  The oracle is
 the fp16 / fp32 CPU restatement: a column-major rocBLAS call D = alpha op(A)
 op(B) + beta C is the row-major engine call (op_a = transB, op_b = transA,
 M = n, N = m, A = b, B = a), the mapping of src/vkblas_hipblas.c:187-189.
-Bars: fp32 normwise <= 1e-5 sqrt(K), fp16 normwise <= 2e-3.
+Bars: fp32 normwise <= 1e-5 sqrt(K), fp16 normwise <= 2e-3, bf16 results
+<= 8e-3 (one bf16 ulp), fp32 results of bf16 inputs <= 2e-3.
 """
 import ctypes
 
@@ -19,7 +20,7 @@ import oracle
 pytestmark = pytest.mark.gpu
 
 OP = {0: 111, 1: 112}            # rocblas_operation none / transpose
-F16, F32, BF16 = 150, 151, 168   # rocblas_datatype
+F16, F32, F64, BF16 = 150, 151, 152, 168   # rocblas_datatype
 HOST, DEVICE = 0, 1              # rocblas_pointer_mode
 
 _vp, _i, _i64, _u32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32
@@ -176,23 +177,83 @@ def test_strided_batched_f16(rh):
         assert normwise(oracle.h2f(got[i * sc: i * sc + m * n]), oracle.h2f(want)) <= F16_BOUND
 
 
+BF_CASES = [(ta, tb, m, n, k, ct) for (m, n, k) in ((64, 48, 40), (257, 129, 65), (512, 256, 256), (8, 1024, 512))
+            for ta in (0, 1) for tb in (0, 1) for ct in (BF16, F32)]
+
+
+@pytest.mark.parametrize("case", BF_CASES, ids=lambda c: f"{'NT'[c[0]]}{'NT'[c[1]]}_{c[2]}x{c[3]}x{c[4]}_"
+                                                          f"{'bf16' if c[5] == BF16 else 'f32'}")
+def test_gemm_ex_bf16(rh, case):
+    """bf16 data (PyTorch's bf16 matmul path): computed by this library, not forwarded."""
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, BF16_BOUND, fbox
+    ta, tb, m, n, k, ct = case
+    print(f"[case] rocblas_gemm_ex bf16 {case}", flush=True)
+    lda = (k if ta else m) + 2
+    ldb = (n if tb else k) + 1
+    ldc = m + 1
+    r = np.random.default_rng(7 + m + k)
+    A = oracle.f2bf_rne((r.standard_normal(lda * (m if ta else k)) / np.sqrt(k)).astype(np.float32))
+    B = oracle.f2bf_rne(r.standard_normal(ldb * (k if tb else n)).astype(np.float32))
+    C32 = r.standard_normal(ldc * n).astype(np.float32)
+    C = oracle.f2bf_rne(C32) if ct == BF16 else C32
+    want = C.copy()
+    fn = oracle.ref_gemm_bf16_rm if ct == BF16 else oracle.ref_gemm_bf16f32_rm
+    fn(tb, ta, n, m, k, B, ldb, A, lda, 1.5, -0.5, want, ldc)
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[ta], OP[tb], m, n, k, fbox(1.5), dA.data_ptr(), BF16, lda, dB.data_ptr(),
+                                BF16, ldb, fbox(-0.5), dC.data_ptr(), ct, ldc, dC.data_ptr(), ct, ldc, F32, 0, 0, 0)
+    assert st == 0
+    got = to_host(dC)
+    g, w = _cols(got, m, n, ldc), _cols(want, m, n, ldc)
+    if ct == BF16:
+        assert normwise(oracle.bf2f(g), oracle.bf2f(w)) <= BF16_BOUND
+    else:
+        assert normwise(g, w) <= F16_BOUND
+    pad = np.ones(got.size, bool)
+    for j in range(n):
+        pad[j * ldc: j * ldc + m] = False
+    assert np.array_equal(got[pad], C[pad])
+
+
+def test_strided_batched_bf16(rh):
+    from gpu_helpers import to_dev, to_host, normwise, BF16_BOUND, fbox
+    m, n, k, nb = 96, 80, 64, 3
+    print("[case] rocblas_gemm_strided_batched_ex bf16", flush=True)
+    sa, sb, sc = m * k + 7, k * n + 5, m * n + 3
+    r = np.random.default_rng(24)
+    A = oracle.f2bf_rne((r.standard_normal(sa * nb) / 8).astype(np.float32))
+    B = oracle.f2bf_rne(r.standard_normal(sb * nb).astype(np.float32))
+    C = oracle.f2bf_rne(r.standard_normal(sc * nb).astype(np.float32))
+    dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
+    st = rh.lib.rocblas_gemm_strided_batched_ex(rh.h, OP[1], OP[0], m, n, k, fbox(1.0), dA.data_ptr(), BF16, k, sa,
+                                                dB.data_ptr(), BF16, k, sb, fbox(1.0), dC.data_ptr(), BF16, m, sc,
+                                                dC.data_ptr(), BF16, m, sc, nb, F32, 0, 0, 0)
+    assert st == 0
+    got = to_host(dC)
+    for i in range(nb):
+        want = C[i * sc: i * sc + m * n].copy()
+        oracle.ref_gemm_bf16_rm(0, 1, n, m, k, B[i * sb:], k, A[i * sa:], k, 1.0, 1.0, want, m)
+        assert normwise(oracle.bf2f(got[i * sc: i * sc + m * n]), oracle.bf2f(want)) <= BF16_BOUND
+
+
 def test_forwarded_calls_still_work(rh):
-    """bf16 (no kernels here) and m == 0 (quick return) reach the real rocBLAS."""
+    """fp64 (no kernels here) and m == 0 (quick return) reach the real rocBLAS."""
     import torch
     from gpu_helpers import fbox
-    print("[case] rocblas_gemm_ex forwarded bf16 / m=0", flush=True)
+    print("[case] rocblas_gemm_ex forwarded f64 / m=0", flush=True)
     m = n = k = 64
-    a = torch.randn(m, k, device="cuda:0").bfloat16()
-    b = torch.randn(k, n, device="cuda:0").bfloat16()
-    c = torch.zeros(n, m, device="cuda:0").bfloat16()
+    a = torch.randn(m, k, device="cuda:0", dtype=torch.float64)
+    b = torch.randn(k, n, device="cuda:0", dtype=torch.float64)
+    c = torch.zeros(n, m, device="cuda:0", dtype=torch.float64)
+    one, zero = ctypes.byref(ctypes.c_double(1.0)), ctypes.byref(ctypes.c_double(0.0))
     # column-major: A^T as stored (k x m col-major = a row-major), C = a @ b in row-major = (b^T a^T)^T
-    st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], n, m, k, fbox(1.0), b.data_ptr(), BF16, n, a.data_ptr(), BF16,
-                                k, fbox(0.0), c.data_ptr(), BF16, n, c.data_ptr(), BF16, n, F32, 0, 0, 0)
+    st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], n, m, k, one, b.data_ptr(), F64, n, a.data_ptr(), F64,
+                                k, zero, c.data_ptr(), F64, n, c.data_ptr(), F64, n, F64, 0, 0, 0)
     assert st == 0
     torch.cuda.synchronize()
-    ref = a.float().cpu() @ b.float().cpu()
-    got = c.float().cpu().reshape(m, n)
-    assert float((got - ref).abs().max() / ref.abs().max()) < 2e-2
+    ref = a.cpu() @ b.cpu()
+    got = c.cpu().reshape(m, n)
+    assert float((got - ref).abs().max() / ref.abs().max()) < 1e-12
     st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], 0, n, k, fbox(1.0), b.data_ptr(), F16, n, a.data_ptr(), F16,
                                 k, fbox(0.0), c.data_ptr(), F16, n, c.data_ptr(), F16, n, F32, 0, 0, 0)
     assert st == 0

@@ -48,13 +48,24 @@ out["mm_f16"] = rel(h1 @ h2, h1.cpu().double() @ h2.cpu().double())
 # fp16 decode linear: W (O, K) row-major = hipBLAS TA=T, the skinny path
 W = (torch.randn(4096, 2048, device=dev) * 0.02).half(); x = torch.randn(4, 2048, device=dev).half()
 out["linear_decode_f16"] = rel(torch.nn.functional.linear(x, W), x.cpu().double() @ W.cpu().double().t())
+# bf16 matmul, bmm and linear (hipblasGemmEx / GemmStridedBatchedEx with 16BF data).
+# A linear with a bias is left out: PyTorch computes that one with a fused
+# bias epilogue in another library, not through hipBLAS / rocBLAS.
+g1 = (torch.randn(384, 1024, device=dev) / 32).bfloat16(); g2 = torch.randn(1024, 640, device=dev).bfloat16()
+out["mm_bf16"] = rel(g1 @ g2, g1.cpu().double() @ g2.cpu().double())
+G1 = torch.randn(4, 128, 256, device=dev).bfloat16(); G2 = (torch.randn(4, 256, 96, device=dev) / 16).bfloat16()
+out["bmm_bf16"] = rel(torch.bmm(G1, G2), torch.bmm(G1.cpu().double(), G2.cpu().double()))
+Wb = (torch.randn(768, 512, device=dev) * 0.05).bfloat16(); xb = torch.randn(64, 512, device=dev).bfloat16()
+out["linear_bf16"] = rel(torch.nn.functional.linear(xb, Wb), xb.cpu().double() @ Wb.cpu().double().t())
 torch.cuda.synchronize()
 print("RESULT " + json.dumps(out), flush=True)
 """
 
 BOUNDS = {"mm_nn": 1e-5 * 129 ** 0.5, "mm_tn": 1e-5 * 129 ** 0.5, "mm_nt": 1e-5 * 129 ** 0.5,
           "mm_tt": 1e-5 * 129 ** 0.5, "addmm": 1e-5 * 129 ** 0.5, "bmm": 1e-5 * 96 ** 0.5,
-          "mm_f16": 2e-3, "linear_decode_f16": 2e-3}
+          "mm_f16": 2e-3, "linear_decode_f16": 2e-3,
+          # bf16 results: one rounding to bf16 (2^-8 relative) plus fp32 sums
+          "mm_bf16": 8e-3, "bmm_bf16": 8e-3, "linear_bf16": 8e-3}
 
 
 def test_torch_ops_go_through_the_library():
@@ -68,12 +79,13 @@ def test_torch_ops_go_through_the_library():
     res = json.loads(line[len("RESULT "):])
     for k, bound in BOUNDS.items():
         assert res[k] <= bound, (k, res[k], bound)
-    # every op above is one intercepted GEMM call: fp32 through the hipBLAS
-    # symbols, fp16 through rocblas_gemm_ex (PyTorch's fp16 path on ROCm)
+    # every op above is one intercepted GEMM call: fp32 and bf16 through the
+    # hipBLAS symbols, fp16 through rocblas_gemm_ex (PyTorch's paths on ROCm)
     calls = [l for l in r.stderr.splitlines() if l.startswith(("[vkblas] hipblas gemm", "[vkblas] rocblas gemm"))]
     assert len(calls) >= len(BOUNDS), r.stderr[-4000:]
     assert "forwarding" not in r.stderr, r.stderr[-4000:]
     assert any("f16->f16" in l for l in calls), calls
+    assert any("bf16->bf16" in l for l in calls), calls
     assert any("batch=8" in l for l in calls), calls
     engine = [l for l in r.stderr.splitlines() if l.startswith("[vkblas] gemm ")]
     assert any("path=skinny" in l for l in engine), engine

@@ -253,3 +253,111 @@ def test_rm_rows_subset():
             assert np.array_equal(part[seg], full[seg])
         else:
             assert np.all(part[seg] == 5.0)
+
+
+# ---------------------------------------------------------------- bf16 bits
+
+def _torch_bf16_bits(x):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy() \
+        .view(np.uint16)
+
+
+def test_bf2f_exhaustive_vs_torch():
+    import torch
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.bf2f(bits)
+    want = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def _bf16_probe_values():
+    r = np.random.default_rng(12)
+    base = r.standard_normal(200000).astype(np.float32)
+    # exact ties between neighbouring bf16 values: low half exactly 0x8000,
+    # with even and odd kept bits
+    tie_bits = (r.integers(0x00800000, 0x7f000000, 20000, dtype=np.uint32) & 0xffff0000) | 0x8000
+    ties = np.concatenate([tie_bits, tie_bits | 0x80000000]).view(np.float32)
+    return np.concatenate([
+        base, base * np.float32(1e-38), base * np.float32(3e38), ties,
+        np.array([3.3895314e38, 3.4028235e38, 1e-45, -1e-45, 0.0, -0.0, np.inf, -np.inf], np.float32),
+        np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float32),
+    ])
+
+
+def test_f2bf_rne_vs_torch():
+    """torch's float -> bfloat16 conversion rounds to nearest even; the oracle
+    must agree bit for bit on normals, subnormals, ties, overflow and infinities."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        x = _bf16_probe_values()
+    x = x[~np.isnan(x)]
+    assert np.array_equal(oracle.f2bf_rne(x), _torch_bf16_bits(x))
+    nan = oracle.f2bf_rne(np.array([np.nan, -np.nan], np.float32))
+    assert np.all(np.isnan(oracle.bf2f(nan)))
+
+
+def test_f2bf_check_catches_truncation():
+    """Truncating instead of rounding (or rounding ties up) fails the torch
+    comparison above on the tie and near-tie probes."""
+    with np.errstate(over="ignore", invalid="ignore"):
+        x = _bf16_probe_values()
+    x = x[np.isfinite(x)]
+    want = _torch_bf16_bits(x)
+    u = x.view(np.uint32)
+    trunc = (u >> 16).astype(np.uint16)
+    ties_up = ((u + np.uint32(0x8000)) >> 16).astype(np.uint16)
+    assert not np.array_equal(trunc, want)
+    assert not np.array_equal(ties_up, want)
+
+
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(4, 4, 4), (33, 65, 17), (64, 1, 64), (1, 40, 300)])
+def test_ref_gemm_bf16_rm_matches_numpy(op_a, op_b, M, N, K):
+    """bf16 GEMM oracle vs numpy float64 on the decoded inputs, rounded by torch."""
+    lda = (M if op_a else K) + 1
+    ldb = (K if op_b else N) + 2
+    ldc = N + 1
+    A = oracle.f2bf_rne(rng(40, lda * (K if op_a else M)))
+    B = oracle.f2bf_rne(rng(41, ldb * (N if op_b else K)))
+    C = oracle.f2bf_rne(rng(42, ldc * M))
+    got = C.copy()
+    oracle.ref_gemm_bf16_rm(op_a, op_b, M, N, K, A, lda, B, ldb, 0.75, 0.5, got, ldc)
+    s = numpy_rm(op_a, op_b, M, N, K, oracle.bf2f(A), lda, oracle.bf2f(B), ldb)
+    old = oracle.bf2f(C)
+    want = C.copy()
+    want32 = old.copy()
+    for i in range(M):
+        sl = slice(i * ldc, i * ldc + N)
+        v = np.float32(0.75) * s[i].astype(np.float32) + np.float32(0.5) * old[sl]
+        want[sl] = _torch_bf16_bits(v)
+        want32[sl] = v
+    assert np.array_equal(got, want)
+    got32 = old.copy()
+    oracle.ref_gemm_bf16f32_rm(op_a, op_b, M, N, K, A, lda, B, ldb, 0.75, 0.5, got32, ldc)
+    assert np.array_equal(got32, want32)
+
+
+def test_ref_gemm_bf16_closed_forms_and_planted_mistakes():
+    """Small integers are exact in bf16 and in the sum: the oracle reproduces
+    the integer product, and fails it with a transposed operand, a dropped
+    beta term or fp16 decoding of the bf16 inputs."""
+    M, N, K = 24, 20, 16
+    Ai = ((np.arange(M * K) * 5) % 9 - 4).astype(np.float32)
+    Bi = ((np.arange(K * N) * 3) % 7 - 3).astype(np.float32)
+    Ci = (np.arange(M * N) % 5).astype(np.float32)
+    A, B, C = oracle.f2bf_rne(Ai), oracle.f2bf_rne(Bi), oracle.f2bf_rne(Ci)
+    exact = Ai.reshape(M, K).astype(np.int64) @ Bi.reshape(K, N).astype(np.int64) + 2 * Ci.reshape(M, N)
+    assert np.abs(exact).max() < 256                    # every result exact in bf16
+
+    def run(op_a, fn=oracle.ref_gemm_bf16_rm, beta=2.0):
+        out = C.copy()
+        fn(op_a, 0, M, N, K, A, K, B, N, 1.0, beta, out, N)
+        return out
+
+    assert np.array_equal(oracle.bf2f(run(0)).reshape(M, N), exact.astype(np.float32))
+    assert not np.array_equal(oracle.bf2f(run(1)).reshape(M, N), exact.astype(np.float32))
+    assert not np.array_equal(oracle.bf2f(run(0, beta=0.0)).reshape(M, N), exact.astype(np.float32))
+    assert not np.array_equal(oracle.bf2f(run(0, fn=oracle.ref_gemm_f16_rm)).reshape(M, N),
+                              exact.astype(np.float32))

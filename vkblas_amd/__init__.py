@@ -29,7 +29,7 @@ STATUS_NAMES = {0: "VKBLAS_OK", 1: "VKBLAS_ERR_INIT", 2: "VKBLAS_ERR_IMPORT", 3:
 # vkblas_op_t
 OP_N, OP_T = 0, 1
 # vkblas_dtype_t
-DT_F32, DT_F16 = 0, 1
+DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 # vkblas_scalar_mode_t
 SCALAR_HOST, SCALAR_DEV_F32, SCALAR_DEV_F16 = 0, 1, 2
 # vkblas_path_t
@@ -132,6 +132,17 @@ def gemm_f32(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1, 
 def gemm_f16(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1, sa=0, sb=0, sc=0) -> int:
     """vkblas_gemm_f16 (reference src/vkblas.h:68-77); returns the status."""
     return load().vkblas_gemm_f16(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, sa, sb, sc)
+
+
+def gemm_bf16(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1, sa=0, sb=0, sc=0) -> int:
+    """vkblas_gemm_bf16 (reference src/vkblas.h:41-50); returns the status."""
+    return load().vkblas_gemm_bf16(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, sa, sb, sc)
+
+
+def gemm_bf16_hipblas(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1, sa=0, sb=0, sc=0) -> int:
+    """vkblas_gemm_bf16_hipblas (reference src/vkblas.h:55-64); returns the status."""
+    return load().vkblas_gemm_bf16_hipblas(op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, sa, sb,
+                                           sc)
 
 
 def hipblas():

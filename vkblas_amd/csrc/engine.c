@@ -101,6 +101,15 @@ static int tile_path(int tile) {
          : tile == VKB_TILE_128 ? VKBLAS_PATH_TILE128 : VKBLAS_PATH_TILE64;
 }
 
+/* vkblas_dtype_t -> kernel element type (vkb_launch.h); the values match */
+static int kernel_type(vkblas_dtype_t t) {
+    return t == VKBLAS_DT_F16 ? VKB_T_F16 : t == VKBLAS_DT_BF16 ? VKB_T_BF16 : VKB_T_F32;
+}
+
+static const char* type_name(int t) {
+    return t == VKB_T_F16 ? "f16" : t == VKB_T_BF16 ? "bf16" : "f32";
+}
+
 /* Tile choice for 256 CUs: the largest tile that still gives about one
  * workgroup per CU; smaller tiles only when the large one would starve. */
 static int choose_tile(uint32_t M, uint32_t N, uint32_t batch) {
@@ -124,7 +133,8 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     memset(plan, 0, sizeof(*plan));
     if (M == 0 || N == 0 || K == 0 || batch == 0) return VKBLAS_ERR_PARAM;
     if (!((ab_type == VKBLAS_DT_F32 && c_type == VKBLAS_DT_F32) ||
-          (ab_type == VKBLAS_DT_F16 && (c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_F32))))
+          (ab_type == VKBLAS_DT_F16 && (c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_F32)) ||
+          (ab_type == VKBLAS_DT_BF16 && (c_type == VKBLAS_DT_BF16 || c_type == VKBLAS_DT_F32))))
         return VKBLAS_ERR_PARAM;
     /* Leading dimensions are taken as given, as the reference engine does
      * (its tests pass lda < M with op_a = T: test/test_h.c:105); only 0 is
@@ -143,7 +153,7 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         return VKBLAS_OK;
     }
 
-    const uint32_t bk = vkb_tile_bk(ab_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32);
+    const uint32_t bk = vkb_tile_bk(kernel_type(ab_type));
     int tile = choose_tile(M, N, batch);
     uint32_t split = 1;
     if (batch == 1) {
@@ -231,13 +241,12 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (st != VKBLAS_OK) return st;
     if (!ensure_init()) return VKBLAS_ERR_INIT;
 
-    const int ab = ab_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32;
-    const int ct = c_type == VKBLAS_DT_F16 ? VKB_T_F16 : VKB_T_F32;
+    const int ab = kernel_type(ab_type);
+    const int ct = kernel_type(c_type);
     int rc = 0;
     if (g_trace)
         fprintf(stderr, "[vkblas] gemm %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s split=%u\n",
-                op_a ? "T" : "N", op_b ? "T" : "N", ab == VKB_T_F16 ? "f16" : "f32",
-                ct == VKB_T_F16 ? "f16" : "f32", M, N, K, lda, ldb, ldc, batch,
+                op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
                 path_name(plan.path), plan.split);
 
     if (plan.path == VKBLAS_PATH_SKINNY) {
@@ -337,11 +346,14 @@ vkblas_status_t vkblas_gemm_bf16(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M,
                                  float alpha, const void* A, uint32_t lda, const void* B, uint32_t ldb,
                                  float beta, void* C, uint32_t ldc, uint32_t batch,
                                  int64_t stride_a, int64_t stride_b, int64_t stride_c) {
-    (void)op_a; (void)op_b; (void)M; (void)N; (void)K; (void)alpha; (void)A; (void)lda; (void)B;
-    (void)ldb; (void)beta; (void)C; (void)ldc; (void)batch; (void)stride_a; (void)stride_b; (void)stride_c;
-    return VKBLAS_ERR_INIT;
+    return finish_sync(vkblas_gemm_async(VKBLAS_DT_BF16, VKBLAS_DT_BF16, op_a, op_b, M, N, K, alpha, A, lda, B,
+                                         ldb, beta, C, ldc, batch, stride_a, stride_b, stride_c, VKBLAS_SCALAR_HOST,
+                                         NULL, NULL, 0, NULL));
 }
 
+/* The reference's second bf16 entry (src/vkblas.c:3448-3512) differs from the
+ * first only in how it avoids a transpose pass of its own; every layout is
+ * read natively here, so both entries are the same call. */
 vkblas_status_t vkblas_gemm_bf16_hipblas(vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N,
                                          uint32_t K, float alpha, const void* A, uint32_t lda, const void* B,
                                          uint32_t ldb, float beta, void* C, uint32_t ldc, uint32_t batch,

@@ -1,4 +1,4 @@
-// gemm_mfma.hpp — blocked MFMA GEMM for gfx950 (CDNA4), fp32 and fp16 inputs.
+// gemm_mfma.hpp — blocked MFMA GEMM for gfx950 (CDNA4), fp32, fp16 and bf16 inputs.
 //
 // Replaces the reference's tiled GLSL GEMMs (gemm_f32_128x128_bankfree_tmpl.comp,
 // gemm_half_128x128_bankfree_tmpl.comp and their 64x64 / 128x256 / split-K
@@ -34,6 +34,8 @@ namespace vkb {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -59,6 +61,31 @@ struct KParams {
 template <typename T> struct Elem;
 template <> struct Elem<float>    { static constexpr int VEC = 4; static constexpr int BK = 32; };
 template <> struct Elem<_Float16> { static constexpr int VEC = 8; static constexpr int BK = 64; };
+template <> struct Elem<__bf16>   { static constexpr int VEC = 8; static constexpr int BK = 64; };
+
+template <typename T> constexpr bool is_bf16 = __is_same(T, __bf16);
+
+// 16-bit MFMAs on raw 16-byte fragments (8 elements of k per lane): fp16 or
+// bf16 by the element type.  srcA / srcB order as the hardware takes them.
+template <typename T>
+__device__ __forceinline__ floatx16 mfma_32x32x16(u32x4 a, u32x4 b, floatx16 c) {
+    if constexpr (is_bf16<T>)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, a),
+                                                      __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ floatx4 mfma_16x16x32(u32x4 a, u32x4 b, floatx4 c) {
+    if constexpr (is_bf16<T>)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                      __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
 
 __device__ __forceinline__ int swz(int row, int chunk) {
     return chunk ^ ((row ^ (row >> 3)) & 7);
@@ -200,6 +227,7 @@ struct Stager {
     }
 };
 
+// Four results to C: fp32 as is, fp16 / bf16 rounded to nearest even.
 template <typename TC>
 __device__ __forceinline__ void store4(TC* p, const float* x, bool vec) {
     if constexpr (sizeof(TC) == 4) {
@@ -210,14 +238,15 @@ __device__ __forceinline__ void store4(TC* p, const float* x, bool vec) {
             for (int i = 0; i < 4; ++i) p[i] = x[i];
         }
     } else {
+        typedef TC v4 __attribute__((ext_vector_type(4)));
         if (vec) {
-            half4_t h;
-            h[0] = (_Float16)x[0]; h[1] = (_Float16)x[1];
-            h[2] = (_Float16)x[2]; h[3] = (_Float16)x[3];
-            *(half4_t*)p = h;
+            v4 h;
+            h[0] = (TC)x[0]; h[1] = (TC)x[1];
+            h[2] = (TC)x[2]; h[3] = (TC)x[3];
+            *(v4*)p = h;
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = (_Float16)x[i];
+            for (int i = 0; i < 4; ++i) p[i] = (TC)x[i];
         }
     }
 }
@@ -233,8 +262,9 @@ __device__ __forceinline__ void load4(const TC* p, float* x, bool vec) {
             for (int i = 0; i < 4; ++i) x[i] = p[i];
         }
     } else {
+        typedef TC v4 __attribute__((ext_vector_type(4)));
         if (vec) {
-            half4_t h = *(const half4_t*)p;
+            v4 h = *(const v4*)p;
 #pragma unroll
             for (int i = 0; i < 4; ++i) x[i] = (float)h[i];
         } else {
@@ -335,8 +365,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(half8_t, bf[j]), __builtin_bit_cast(half8_t, af[i]), acc[i][j], 0, 0, 0);
+                        acc[i][j] = mfma_32x32x16<T>(bf[j], af[i], acc[i][j]);
             }
         } else {
             // v_mfma_f32_32x32x2_f32: lane holds 1 k of one row.  Lane half h

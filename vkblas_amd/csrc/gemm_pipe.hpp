@@ -256,16 +256,12 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
             const int i = q >> 1, j0 = (q & 1) * 4;
 #pragma unroll
             for (int j = j0; j < j0 + 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, bf[buf][j]),
-                                                                  __builtin_bit_cast(half8_t, af[buf % NAB][i]),
-                                                                  acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma_16x16x32<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
         } else if constexpr (SH == 1) {
             const int i = q >> 1, j0 = (q & 1) * 2;
 #pragma unroll
             for (int j = j0; j < j0 + 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8_t, bf[buf][j]),
-                                                                  __builtin_bit_cast(half8_t, af[buf % NAB][i]),
-                                                                  acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma_32x32x16<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
         } else {
             const int e = q >> 1, i0 = (q & 1) * 2;
 #pragma unroll

@@ -2,7 +2,7 @@
  * hipblas_shim.c — hipBLAS ABI entry points of libvkblas_hipblas.so (C11).
  *
  * Drop-in for the reference's LD_PRELOAD shim (src/vkblas_hipblas.c).  The
- * fp32 / fp16 GEMM family is computed by this library's gfx950 kernels; every
+ * fp32 / fp16 / bf16 GEMM family is computed by this library's gfx950 kernels; every
  * other exported hipBLAS symbol, and every GEMM call this library declines,
  * is forwarded to the real hipBLAS of the process.
  *
@@ -178,6 +178,10 @@ static int op_is_t(hipblasOperation_t op) { return op == HIPBLAS_OP_T || op == H
 /* Runs the GEMM on this library's kernels, or returns VKB_DECLINE for the
  * caller to forward.  ab / ct: element types; scal_f16: alpha and beta are
  * hipblasHalf (else float). */
+static const char* dtype_name(vkblas_dtype_t t) {
+    return t == VKBLAS_DT_F16 ? "f16" : t == VKBLAS_DT_BF16 ? "bf16" : "f32";
+}
+
 static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkblas_dtype_t ct, int scal_f16,
                                 hipblasOperation_t transA, hipblasOperation_t transB,
                                 int64_t m, int64_t n, int64_t k, const void* alpha,
@@ -224,8 +228,8 @@ static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkbla
     }
     if (g_trace)
         fprintf(stderr, "[vkblas] hipblas gemm %s%s %s->%s m=%lld n=%lld k=%lld lda=%lld ldb=%lld ldc=%lld batch=%lld\n",
-                op_is_t(transA) ? "T" : "N", op_is_t(transB) ? "T" : "N", ab == VKBLAS_DT_F16 ? "f16" : "f32",
-                ct == VKBLAS_DT_F16 ? "f16" : "f32", (long long)m, (long long)n, (long long)k, (long long)lda,
+                op_is_t(transA) ? "T" : "N", op_is_t(transB) ? "T" : "N", dtype_name(ab), dtype_name(ct),
+                (long long)m, (long long)n, (long long)k, (long long)lda,
                 (long long)ldb, (long long)ldc, (long long)batch);
     vkblas_status_t st = vkblas_gemm_async(
         ab, ct, op_is_t(transB) ? VKBLAS_OP_T : VKBLAS_OP_N, op_is_t(transA) ? VKBLAS_OP_T : VKBLAS_OP_N,
@@ -239,10 +243,11 @@ static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkbla
 }
 
 /* Data / compute type classification.  Values of the pre-3.0
- * hipblasDatatype_t (150 = R_16F, 151 = R_32F) are accepted as well, as the
- * reference did (src/vkblas_hipblas.c:280-284). */
+ * hipblasDatatype_t (150 = R_16F, 151 = R_32F, 168 = R_16B) are accepted as
+ * well, as the reference did (src/vkblas_hipblas.c:280-284). */
 static int is_f32_t(int t) { return t == HIP_R_32F || t == 151; }
 static int is_f16_t(int t) { return t == HIP_R_16F || t == 150; }
+static int is_bf16_t(int t) { return t == HIP_R_16BF || t == 168; }
 /* 1: float scalars, fp32 accumulate; 2: half scalars (COMPUTE_16F);
  * 0: not handled here.  Full-precision fp32 arithmetic is always an allowed
  * implementation of the FAST_* compute types. */
@@ -277,6 +282,15 @@ static int ex_types(int at, int bt, int ctp, int comp, vkblas_dtype_t* ab, vkbla
         *ab = VKBLAS_DT_F16;
         *ct = is_f16_t(ctp) ? VKBLAS_DT_F16 : VKBLAS_DT_F32;
         *scal_f16 = kind == 2;
+        return 1;
+    }
+    /* bf16 (reference src/vkblas_hipblas.c:426-461 routes 16BF -> 16BF; a
+     * 32F result is computed here too).  hipBLAS defines bf16 GEMMs with fp32
+     * compute only, so alpha / beta are floats. */
+    if (is_bf16_t(at) && is_bf16_t(bt) && (is_bf16_t(ctp) || is_f32_t(ctp)) && kind == 1) {
+        *ab = VKBLAS_DT_BF16;
+        *ct = is_bf16_t(ctp) ? VKBLAS_DT_BF16 : VKBLAS_DT_F32;
+        *scal_f16 = 0;
         return 1;
     }
     return 0;

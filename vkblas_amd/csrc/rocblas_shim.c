@@ -20,7 +20,8 @@
  *   - m, n, k or batch_count <= 0 and invalid leading dimensions are forwarded
  *     so rocBLAS's own quick-return and error semantics apply (the reference
  *     returned invalid_value, line 836);
- *   - bf16 is forwarded (this library has no bf16 kernels);
+ *   - bf16 inputs with bf16 or fp32 C / D are computed (the reference
+ *     forwarded rocBLAS bf16 calls);
  *   - the real library is found among the libraries the process already
  *     loaded (RTLD_NEXT, then librocblas.so.5 by soname), not by dlopen of a
  *     fixed path (reference lines 811-819).
@@ -122,9 +123,14 @@ static int op_t(rocblas_operation op) {
     return op == rocblas_operation_transpose || op == rocblas_operation_conjugate_transpose;
 }
 
+static const char* dtype_name(vkblas_dtype_t t) {
+    return t == VKBLAS_DT_F16 ? "f16" : t == VKBLAS_DT_BF16 ? "bf16" : "f32";
+}
+
 static int dtype_of(rocblas_datatype t, vkblas_dtype_t* out) {
     if (t == rocblas_datatype_f32_r) { *out = VKBLAS_DT_F32; return 1; }
     if (t == rocblas_datatype_f16_r) { *out = VKBLAS_DT_F16; return 1; }
+    if (t == rocblas_datatype_bf16_r) { *out = VKBLAS_DT_BF16; return 1; }
     return 0;
 }
 
@@ -179,14 +185,14 @@ static int run(const gemm_call* g) {
     if (g_trace)
         fprintf(stderr, "[vkblas] rocblas gemm %s%s %s->%s m=%lld n=%lld k=%lld lda=%lld ldb=%lld ldc=%lld ldd=%lld "
                         "batch=%lld\n",
-                op_t(g->transA) ? "T" : "N", op_t(g->transB) ? "T" : "N", ab == VKBLAS_DT_F16 ? "f16" : "f32",
-                ct == VKBLAS_DT_F16 ? "f16" : "f32", (long long)g->m, (long long)g->n, (long long)g->k,
+                op_t(g->transA) ? "T" : "N", op_t(g->transB) ? "T" : "N", dtype_name(ab), dtype_name(ct),
+                (long long)g->m, (long long)g->n, (long long)g->k,
                 (long long)g->lda, (long long)g->ldb, (long long)g->ldc, (long long)g->ldd, (long long)g->batch);
 
     /* D separate from C: bring C into D first when the epilogue may read it */
     if (g->c != g->d && beta_maybe_nonzero) {
         if (!g->c) return 1;
-        const size_t es = ct == VKBLAS_DT_F16 ? 2 : 4;
+        const size_t es = ct == VKBLAS_DT_F32 ? 4 : 2;
         for (int64_t i = 0; i < g->batch; ++i) {
             if (hipMemcpy2DAsync((char*)g->d + (size_t)(i * g->sd) * es, (size_t)g->ldd * es,
                                  (const char*)g->c + (size_t)(i * g->sc) * es, (size_t)g->ldc * es,

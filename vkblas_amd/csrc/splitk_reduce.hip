@@ -3,7 +3,7 @@
 // Pass 2 replaces the reference's splitk_reduce_f32.comp / splitk_reduce_hgemm.comp
 // (reduce loop src/shaders/splitk_reduce_f32.comp:15-24): every output sums its
 // fp32 partials in the fixed order s = 0 .. split-1, then applies alpha / beta
-// and rounds once to the output type.  No atomics, so results are bitwise
+// and rounds once to the output type (fp32, fp16 or bf16).  No atomics, so results are bitwise
 // reproducible run to run.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -12,6 +12,8 @@
 extern "C" int vkb_launch_gemm_f32_impl(const vkb_gemm_args* a, int tile, void* stream);
 extern "C" int vkb_launch_gemm_f16h_impl(const vkb_gemm_args* a, int tile, void* stream);
 extern "C" int vkb_launch_gemm_f16s_impl(const vkb_gemm_args* a, int tile, void* stream);
+extern "C" int vkb_launch_gemm_bf16h_impl(const vkb_gemm_args* a, int tile, void* stream);
+extern "C" int vkb_launch_gemm_bf16s_impl(const vkb_gemm_args* a, int tile, void* stream);
 
 namespace {
 
@@ -84,10 +86,16 @@ extern "C" int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, ui
         hipLaunchKernelGGL(splitk_reduce_kernel<float>, dim3((uint32_t)blocks), dim3(256), 0, st, P,
                            stride_split, split, M, N, (float*)C, ldc, alpha, beta, scalar_mode,
                            alpha_dev, beta_dev);
-    } else {
+    } else if (c_type == VKB_T_F16) {
         hipLaunchKernelGGL(splitk_reduce_kernel<_Float16>, dim3((uint32_t)blocks), dim3(256), 0, st, P,
                            stride_split, split, M, N, (_Float16*)C, ldc, alpha, beta, scalar_mode,
                            alpha_dev, beta_dev);
+    } else if (c_type == VKB_T_BF16) {
+        hipLaunchKernelGGL(splitk_reduce_kernel<__bf16>, dim3((uint32_t)blocks), dim3(256), 0, st, P,
+                           stride_split, split, M, N, (__bf16*)C, ldc, alpha, beta, scalar_mode,
+                           alpha_dev, beta_dev);
+    } else {
+        return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
 }
@@ -96,11 +104,13 @@ extern "C" uint32_t vkb_tile_bm(int tile) {
     return tile == VKB_TILE_256 ? 256u : tile == VKB_TILE_128 ? 128u : 64u;
 }
 extern "C" uint32_t vkb_tile_bn(int tile) { return vkb_tile_bm(tile); }
-extern "C" uint32_t vkb_tile_bk(int ab_type) { return ab_type == VKB_T_F16 ? 64u : 32u; }
+extern "C" uint32_t vkb_tile_bk(int ab_type) { return ab_type == VKB_T_F32 ? 32u : 64u; }
 
 extern "C" int vkb_launch_gemm(const vkb_gemm_args* a, int tile, void* stream) {
     if (a->ab_type == VKB_T_F32 && a->c_type == VKB_T_F32) return vkb_launch_gemm_f32_impl(a, tile, stream);
     if (a->ab_type == VKB_T_F16 && a->c_type == VKB_T_F16) return vkb_launch_gemm_f16h_impl(a, tile, stream);
     if (a->ab_type == VKB_T_F16 && a->c_type == VKB_T_F32) return vkb_launch_gemm_f16s_impl(a, tile, stream);
+    if (a->ab_type == VKB_T_BF16 && a->c_type == VKB_T_BF16) return vkb_launch_gemm_bf16h_impl(a, tile, stream);
+    if (a->ab_type == VKB_T_BF16 && a->c_type == VKB_T_F32) return vkb_launch_gemm_bf16s_impl(a, tile, stream);
     return (int)hipErrorInvalidValue;
 }

@@ -19,7 +19,7 @@ extern "C" {
 #endif
 
 /* element types (values match vkblas_dtype_t in vkblas_ext.h) */
-enum { VKB_T_F32 = 0, VKB_T_F16 = 1 };
+enum { VKB_T_F32 = 0, VKB_T_F16 = 1, VKB_T_BF16 = 2 };
 
 /* how alpha / beta reach the kernel */
 enum { VKB_SCALAR_HOST = 0, VKB_SCALAR_DEV_F32 = 1, VKB_SCALAR_DEV_F16 = 2 };
@@ -63,7 +63,7 @@ uint32_t vkb_tile_bn(int tile);
 uint32_t vkb_tile_bk(int ab_type);
 
 /* Blocked MFMA GEMM for all four layouts.  ab_type F32 -> c_type F32;
- * ab_type F16 -> c_type F16 or F32. */
+ * ab_type F16 -> c_type F16 or F32; ab_type BF16 -> c_type BF16 or F32. */
 int vkb_launch_gemm(const vkb_gemm_args* a, int tile, void* stream);
 
 /* Split-K pass 2: C = alpha * sum_{s=0}^{split-1} P[s] + beta * C, summed in
