@@ -1,10 +1,11 @@
 """Edge cases of the decode kernels (engine op_a = N, op_b = T, M <= 16: the
-GEMV kernel for M <= 4, the MFMA skinny kernel above), the path the
+GEMV kernel for M <= 2, the MFMA skinny kernel above; fp16 and bf16), the path the
 reference reaches for matvec / skinny shapes (src/vkblas.c:2100-2392,
 2501-2808).  Ragged K (not a multiple of the kernels' K steps), padded
 leading dimensions whose padding holds NaN (it must never reach C), beta != 0,
-fp32 output and device-memory scalars; the oracle is the fp16 CPU
-restatement.  Bar: normwise <= 2e-3.
+fp32 output and device-memory scalars; the oracle is the fp16 / bf16 CPU
+restatement.  Bars: fp16 and fp32 results normwise <= 2e-3, bf16 results
+<= 8e-3 (one bf16 ulp).
 """
 import numpy as np
 import pytest
@@ -13,14 +14,22 @@ import oracle
 
 pytestmark = pytest.mark.gpu
 
-NAN16 = np.uint16(0x7E00)
+NAN16 = np.uint16(0x7E00)     # quiet NaN, fp16 encoding
+NAN_BF16 = np.uint16(0x7FC0)  # quiet NaN, bf16 encoding
 
 CASES = []
 for M in (1, 2, 3, 4, 5, 8, 16):
     for (N, K) in ((1, 8), (7, 504), (100, 520), (1000, 1032), (300, 4104), (64, 8192)):
         CASES.append((M, N, K, 0, 0, 0.0, "f16"))
+for M in (1, 2, 3, 8, 16):
+    for (N, K) in ((7, 504), (1000, 1032), (300, 4104)):
+        CASES.append((M, N, K, 0, 0, 0.0, "bf16"))
 CASES += [
     (1, 1000, 1032, 8, 16, 0.0, "f16"),
+    (1, 777, 1000, 16, 8, 0.5, "bf16"),
+    (5, 640, 2056, 8, 24, -0.5, "bf16"),
+    (2, 1024, 2048, 0, 0, 0.25, "bf16>f32"),
+    (12, 512, 520, 8, 0, 1.0, "bf16>f32"),
     (3, 333, 4104, 24, 8, -0.5, "f16"),
     (4, 1024, 2048, 0, 0, 0.25, "f32"),
     (8, 777, 1000, 16, 8, -0.5, "f16"),
@@ -29,12 +38,13 @@ CASES += [
 ]
 
 
-def _padded(rows, cols, ld, seed, scale):
-    """rows x cols fp16 matrix in a buffer of (rows-1)*ld + cols elements,
-    NaN in the padding between rows."""
+def _padded(rows, cols, ld, seed, scale, bf=False):
+    """rows x cols fp16 (bf16 if bf) matrix in a buffer of (rows-1)*ld + cols
+    elements, NaN in the padding between rows."""
     r = np.random.default_rng(seed)
-    buf = np.full((rows - 1) * ld + cols, NAN16, np.uint16)
-    vals = oracle.f2h_rne((r.standard_normal(rows * cols) * scale).astype(np.float32))
+    buf = np.full((rows - 1) * ld + cols, NAN_BF16 if bf else NAN16, np.uint16)
+    conv = oracle.f2bf_rne if bf else oracle.f2h_rne
+    vals = conv((r.standard_normal(rows * cols) * scale).astype(np.float32))
     for i in range(rows):
         buf[i * ld: i * ld + cols] = vals[i * cols:(i + 1) * cols]
     return buf
@@ -44,34 +54,36 @@ def _padded(rows, cols, ld, seed, scale):
 def test_decode_edges(case):
     import torch
     import vkblas_amd as vk
-    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, BF16_BOUND
     M, N, K, pad_a, pad_b, beta, out = case
     print(f"[case] decode edge {case}", flush=True)
+    bf = out.startswith("bf16")
+    f32 = out.endswith("f32")
     lda, ldb, ldc = K + pad_a, K + pad_b, N
-    hX = _padded(M, K, lda, 1 + M + K, 1.0)
-    hW = _padded(N, K, ldb, 2 + N + K, 0.05)
-    f16 = out == "f16"
+    hX = _padded(M, K, lda, 1 + M + K, 1.0, bf)
+    hW = _padded(N, K, ldb, 2 + N + K, 0.05, bf)
     r = np.random.default_rng(3)
-    if f16:
-        hC = oracle.f2h_rne(r.standard_normal(M * ldc).astype(np.float32))
-    else:
-        hC = r.standard_normal(M * ldc).astype(np.float32)
+    c = r.standard_normal(M * ldc).astype(np.float32)
+    hC = c if f32 else (oracle.f2bf_rne(c) if bf else oracle.f2h_rne(c))
     want = hC.copy()
-    if f16:
-        oracle.ref_gemm_f16_rm(0, 1, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
+    if bf:
+        ref = oracle.ref_gemm_bf16f32_rm if f32 else oracle.ref_gemm_bf16_rm
     else:
-        oracle.ref_gemm_f16f32_rm(0, 1, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
+        ref = oracle.ref_gemm_f16f32_rm if f32 else oracle.ref_gemm_f16_rm
+    ref(0, 1, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
     dX, dW, dC = to_dev(hX), to_dev(hW), to_dev(hC)
-    vk.gemm_async(vk.DT_F16, vk.DT_F16 if f16 else vk.DT_F32, vk.OP_N, vk.OP_T, M, N, K, 1.5, dX.data_ptr(), lda,
+    ab = vk.DT_BF16 if bf else vk.DT_F16
+    vk.gemm_async(ab, vk.DT_F32 if f32 else ab, vk.OP_N, vk.OP_T, M, N, K, 1.5, dX.data_ptr(), lda,
                   dW.data_ptr(), ldb, beta, dC.data_ptr(), ldc, stream=torch.cuda.current_stream().cuda_stream)
     assert vk.last_path() == vk.PATH_SKINNY
     got = to_host(dC)
-    if f16:
-        g, w = oracle.h2f(got), oracle.h2f(want)
-    else:
+    if f32:
         g, w = got, want
+    else:
+        dec = oracle.bf2f if bf else oracle.h2f
+        g, w = dec(got), dec(want)
     assert np.all(np.isfinite(g))
-    assert normwise(g, w) <= F16_BOUND
+    assert normwise(g, w) <= (BF16_BOUND if bf and not f32 else F16_BOUND)
 
 
 @pytest.mark.parametrize("M", [1, 4, 12])

@@ -57,6 +57,9 @@ G1 = torch.randn(4, 128, 256, device=dev).bfloat16(); G2 = (torch.randn(4, 256, 
 out["bmm_bf16"] = rel(torch.bmm(G1, G2), torch.bmm(G1.cpu().double(), G2.cpu().double()))
 Wb = (torch.randn(768, 512, device=dev) * 0.05).bfloat16(); xb = torch.randn(64, 512, device=dev).bfloat16()
 out["linear_bf16"] = rel(torch.nn.functional.linear(xb, Wb), xb.cpu().double() @ Wb.cpu().double().t())
+# bf16 decode linear (2 tokens): the skinny path
+xd = torch.randn(2, 512, device=dev).bfloat16()
+out["linear_decode_bf16"] = rel(torch.nn.functional.linear(xd, Wb), xd.cpu().double() @ Wb.cpu().double().t())
 torch.cuda.synchronize()
 print("RESULT " + json.dumps(out), flush=True)
 """
@@ -65,7 +68,7 @@ BOUNDS = {"mm_nn": 1e-5 * 129 ** 0.5, "mm_tn": 1e-5 * 129 ** 0.5, "mm_nt": 1e-5 
           "mm_tt": 1e-5 * 129 ** 0.5, "addmm": 1e-5 * 129 ** 0.5, "bmm": 1e-5 * 96 ** 0.5,
           "mm_f16": 2e-3, "linear_decode_f16": 2e-3,
           # bf16 results: one rounding to bf16 (2^-8 relative) plus fp32 sums
-          "mm_bf16": 8e-3, "bmm_bf16": 8e-3, "linear_bf16": 8e-3}
+          "mm_bf16": 8e-3, "bmm_bf16": 8e-3, "linear_bf16": 8e-3, "linear_decode_bf16": 8e-3}
 
 
 def test_torch_ops_go_through_the_library():
@@ -88,7 +91,8 @@ def test_torch_ops_go_through_the_library():
     assert any("bf16->bf16" in l for l in calls), calls
     assert any("batch=8" in l for l in calls), calls
     engine = [l for l in r.stderr.splitlines() if l.startswith("[vkblas] gemm ")]
-    assert any("path=skinny" in l for l in engine), engine
+    assert any("path=skinny" in l and "f16->f16" in l and "bf16" not in l for l in engine), engine
+    assert any("path=skinny" in l and "bf16->bf16" in l for l in engine), engine
 
 
 def test_unmodified_script_through_the_runner(tmp_path):

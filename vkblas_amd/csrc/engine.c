@@ -142,8 +142,8 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (lda == 0 || ldb == 0 || ldc == 0) return VKBLAS_ERR_PARAM;
     if (split_k == 0 && g_force_split) split_k = g_force_split;
 
-    /* decode-shaped fp16: X[M<=16, K] . W[N, K]^T, both K-contiguous */
-    if (ab_type == VKBLAS_DT_F16 && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 16 &&
+    /* decode-shaped fp16 / bf16: X[M<=16, K] . W[N, K]^T, both K-contiguous */
+    if ((ab_type == VKBLAS_DT_F16 || ab_type == VKBLAS_DT_BF16) && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 16 &&
         batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && lda >= K && ldb >= K &&
         !g_no_skinny) {
         plan->path = VKBLAS_PATH_SKINNY;
@@ -250,7 +250,7 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 path_name(plan.path), plan.split);
 
     if (plan.path == VKBLAS_PATH_SKINNY) {
-        rc = vkb_launch_skinny_f16(A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
+        rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
                                    alpha_dev, beta_dev, stream);
     } else {
         vkb_gemm_args a;

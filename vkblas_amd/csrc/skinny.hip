@@ -1,4 +1,4 @@
-// skinny_f16.hip — bandwidth-bound fp16 skinny GEMM / matvec for decode.
+// skinny.hip — bandwidth-bound fp16 / bf16 skinny GEMM / matvec for decode.
 //
 // Replaces the reference's matvec family (src/vkblas.c:2100-2392, 2501-2808;
 // shaders matvec_splitk_tmpl.comp, matvec_splitk_m_tmpl.comp and the
@@ -13,7 +13,7 @@
 // Work decomposition: a workgroup owns R tiles of 16 weight rows; its WAVES
 // waves split K into contiguous slices.  Per 128-wide K step a lane streams
 // four 16-byte pieces of one weight row and of one activation row, and feeds
-// four v_mfma_f32_16x16x32_f16 per row tile (src A = 16 weight rows, src B =
+// four v_mfma_f32_16x16x32_{f16,bf16} per row tile (src A = 16 weight rows, src B =
 // up to 16 activation rows).  Lane group g = lane/16 of load / MFMA j takes k
 // in [128 c + 32 j + 8 g, +8): the same k for both operands, every k exactly
 // once, and each load instruction reads 64 contiguous bytes of each of its 16
@@ -35,12 +35,35 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Element type T of X and W (_Float16 or __bf16): the two 16-bit products.
+template <typename T>
+__device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b, floatx4 c) {
+    if constexpr (__is_same(T, __bf16))
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                       __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a),
+                                                      __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
+}
+
+// a + w.lo * x.lo + w.hi * x.hi (v_dot2_f32_f16 / v_dot2c_f32_bf16)
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float a) {
+    if constexpr (__is_same(T, __bf16))
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), a,
+                                               false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x), a, false);
+}
+
 struct SkParams {
-    const _Float16* X;
-    const _Float16* W;
+    const uint16_t* X;   // 16-bit elements (fp16 or bf16 bit patterns)
+    const uint16_t* W;
     void* C;
     int64_t lda, ldb, ldc;
     uint32_t M, N, K;
@@ -50,17 +73,17 @@ struct SkParams {
     const void* beta_dev;
 };
 
-__device__ __forceinline__ u32x4 ld8_checked(const _Float16* p, int nvalid) {
+__device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
     if (nvalid >= 8) return *(const u32x4*)p;
     uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        if (i < nvalid) w[i >> 1] |= (uint32_t)(*(const uint16_t*)(p + i)) << (16 * (i & 1));
+        if (i < nvalid) w[i >> 1] |= (uint32_t)p[i] << (16 * (i & 1));
     return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-template <typename TC, int R, int WAVES, int D>
-__global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
+template <typename T, typename TC, int R, int WAVES, int D>
+__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkParams p) {
     __shared__ float red[WAVES][R][4][64];
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -107,8 +130,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wv[slot][r][j]),
-                                                               __builtin_bit_cast(half8_t, xv[slot][j]), acc[r], 0, 0, 0);
+                acc[r] = mfma16<T>(wv[slot][r][j], xv[slot][j], acc[r]);
     };
 
     // full K steps [c_beg, c_full_end): rolling window of D steps.  Each
@@ -164,8 +186,7 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, wt[r][j]),
-                                                               __builtin_bit_cast(half8_t, xt[j]), acc[r], 0, 0, 0);
+                acc[r] = mfma16<T>(wt[r][j], xt[j], acc[r]);
     }
 
 #pragma unroll
@@ -207,13 +228,14 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_f16_kernel(SkParams p) {
 // lines, loaded non-temporal: the weights stream through once, and whole-line
 // requests let nt skip the cache without re-fetching the other half of a
 // line): lane l takes k in [c*512 + 8 l, +8) of chunk c and multiplies it
-// with the same k of each activation row (v_dot2_f32_f16, fp32 accumulate).
+// with the same k of each activation row (v_dot2_f32_f16 / v_dot2c_f32_bf16,
+// fp32 accumulate).
 // Workgroup: 4 waves, RB weight rows; wave w takes chunks w, w+4, ... of K,
 // loading the next chunk's RB rows while it computes the current one.
 // Partials (MM x RB per lane) are summed across the 64 lanes by a butterfly
 // reduce-scatter, then across the 4 waves in wave order: deterministic.
-template <typename TC, int MM, int RB>
-__global__ __launch_bounds__(256) void gemv_f16_kernel(SkParams p) {
+template <typename T, typename TC, int MM, int RB>
+__global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
     constexpr int P = MM * RB;                    // partials per lane (power of 2, <= 64)
     constexpr int LP = P == 2 ? 1 : P == 4 ? 2 : P == 8 ? 3 : P == 16 ? 4 : P == 32 ? 5 : 6;
     static_assert((1 << LP) == P, "MM * RB must be a power of 2 in [2, 64]");
@@ -263,8 +285,7 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(SkParams p) {
                     // element copied out first: a bit cast of a vector
                     // subscript compiled to element 0 for every e
                     const uint32_t we = wr[e], xe = xm[e];
-                    a = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, we), __builtin_bit_cast(half2_t, xe), a,
-                                               false);
+                    a = dot2<T>(we, xe, a);
                 }
                 acc[m][r] = a;
             }
@@ -334,51 +355,60 @@ __global__ __launch_bounds__(256) void gemv_f16_kernel(SkParams p) {
     }
 }
 
-template <typename TC, int MM, int RB>
+template <typename T, typename TC, int MM, int RB>
 int launch_gemv(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + RB - 1) / RB;
-    hipLaunchKernelGGL((gemv_f16_kernel<TC, MM, RB>), dim3(grid), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((gemv_kernel<T, TC, MM, RB>), dim3(grid), dim3(256), 0, st, p);
     return (int)hipGetLastError();
 }
 
-template <typename TC, int R, int WAVES, int D>
+template <typename T, typename TC, int R, int WAVES, int D>
 int launch_sk(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
-    hipLaunchKernelGGL((skinny_f16_kernel<TC, R, WAVES, D>), dim3(grid), dim3(WAVES * 64), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<T, TC, R, WAVES, D>), dim3(grid), dim3(WAVES * 64), 0, st, p);
     return (int)hipGetLastError();
+}
+
+// One element type: output fp32 or the input type.
+//   M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best for
+//   4096-14336 rows); more activation rows multiply its VALU work and
+//   registers, and the MFMA kernel is faster from M = 3 on.
+//   M > 2: four waves split K with four steps in flight.  One 16-row tile per
+//   workgroup maximises workgroups; with more than 4 activation rows, two
+//   tiles share each activation load when that still leaves >= 256
+//   workgroups (one per CU).
+template <typename T>
+int launch_typed(const SkParams& p, bool f32_out, hipStream_t st) {
+    if (p.M <= 2) {
+        if (f32_out) return p.M == 1 ? launch_gemv<T, float, 1, 4>(p, st) : launch_gemv<T, float, 2, 4>(p, st);
+        return p.M == 1 ? launch_gemv<T, T, 1, 4>(p, st) : launch_gemv<T, T, 2, 4>(p, st);
+    }
+    const bool two = p.M > 4 && (p.N + 31) / 32 >= 256;
+    if (f32_out) return two ? launch_sk<T, float, 2, 4, 4>(p, st) : launch_sk<T, float, 1, 4, 4>(p, st);
+    return two ? launch_sk<T, T, 2, 4, 4>(p, st) : launch_sk<T, T, 1, 4, 4>(p, st);
 }
 
 }  // namespace
 
-extern "C" int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, int64_t ldb,
-                                     void* C, int64_t ldc, int c_type,
-                                     uint32_t M, uint32_t N, uint32_t K,
-                                     float alpha, float beta, int scalar_mode,
-                                     const void* alpha_dev, const void* beta_dev, void* stream) {
+extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
+                                 void* C, int64_t ldc, int c_type,
+                                 uint32_t M, uint32_t N, uint32_t K,
+                                 float alpha, float beta, int scalar_mode,
+                                 const void* alpha_dev, const void* beta_dev, void* stream) {
     if (M == 0 || M > 16 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
+    if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) return (int)hipErrorInvalidValue;
+    if (c_type != VKB_T_F32 && c_type != ab_type) return (int)hipErrorInvalidValue;
     if ((lda & 7) || (ldb & 7) || ((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
     // buffer offsets are 32-bit: a 32-row weight tile and the activations
     // must span less than 2 GiB
     if ((uint64_t)32 * ldb * 2 >= (1ull << 31) || (uint64_t)M * lda * 2 >= (1ull << 31)) return (int)hipErrorInvalidValue;
     SkParams p;
-    p.X = (const _Float16*)X; p.W = (const _Float16*)W; p.C = C;
+    p.X = (const uint16_t*)X; p.W = (const uint16_t*)W; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.M = M; p.N = N; p.K = K;
     p.alpha = alpha; p.beta = beta; p.mode = scalar_mode;
     p.alpha_dev = alpha_dev; p.beta_dev = beta_dev;
     hipStream_t st = (hipStream_t)stream;
-    // Four waves split K with four steps in flight.  One 16-row tile per
-    // workgroup maximises workgroups; with more than 4 activation rows, two
-    // tiles share each activation load when that still leaves >= 256
-    // workgroups (one per CU).
-    // M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best
-    // for 4096-14336 rows); more activation rows multiply its VALU work and
-    // registers, and the MFMA kernel is faster from M = 3 on.
-    if (M <= 2) {
-        if (c_type == VKB_T_F32) return M == 1 ? launch_gemv<float, 1, 4>(p, st) : launch_gemv<float, 2, 4>(p, st);
-        return M == 1 ? launch_gemv<_Float16, 1, 4>(p, st) : launch_gemv<_Float16, 2, 4>(p, st);
-    }
-    const bool two = M > 4 && (N + 31) / 32 >= 256;
-    if (c_type == VKB_T_F32) return two ? launch_sk<float, 2, 4, 4>(p, st) : launch_sk<float, 1, 4, 4>(p, st);
-    return two ? launch_sk<_Float16, 2, 4, 4>(p, st) : launch_sk<_Float16, 1, 4, 4>(p, st);
+    const bool f32_out = c_type == VKB_T_F32;
+    return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, st) : launch_typed<_Float16>(p, f32_out, st);
 }

@@ -74,15 +74,16 @@ int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t spli
                              float alpha, float beta, int scalar_mode,
                              const void* alpha_dev, const void* beta_dev, void* stream);
 
-/* Skinny fp16 GEMM for decode (M <= 16 rows of activations):
+/* Skinny 16-bit GEMM for decode (M <= 16 rows of activations):
  *   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n]
- * X = A (K-contiguous rows, lda), W = B (K-contiguous rows, ldb).
- * Requires lda, ldb multiples of 8 and 16-byte aligned A, B. */
-int vkb_launch_skinny_f16(const void* X, int64_t lda, const void* W, int64_t ldb,
-                          void* C, int64_t ldc, int c_type,
-                          uint32_t M, uint32_t N, uint32_t K,
-                          float alpha, float beta, int scalar_mode,
-                          const void* alpha_dev, const void* beta_dev, void* stream);
+ * X = A (K-contiguous rows, lda), W = B (K-contiguous rows, ldb); ab_type F16
+ * or BF16, c_type F32 or ab_type.  Requires lda, ldb multiples of 8 and
+ * 16-byte aligned A, B. */
+int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
+                      void* C, int64_t ldc, int c_type,
+                      uint32_t M, uint32_t N, uint32_t K,
+                      float alpha, float beta, int scalar_mode,
+                      const void* alpha_dev, const void* beta_dev, void* stream);
 
 #ifdef __cplusplus
 }
