@@ -12,7 +12,7 @@ fp16 MFMA peak, 8192x8192 fp16 decode matvec vs HBM peak, with three weight
 copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|matvec|splitk|batched]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched]
 """
 import argparse
 import json
@@ -101,17 +101,20 @@ def fp32_headline(torch, vk, stream, steps, warmup):
             "tflops_by_variant": by_variant, "launches": len(per)}
 
 
-def fp16_gemm(torch, vk, stream, steps, n=4096):
-    """configs[2] sample: fp16 GemmEx 16F x 16F -> 16F, NN and TN."""
+def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False):
+    """configs[2] sample: fp16 GemmEx 16F x 16F -> 16F, NN and TN (bf16: the
+    same with 16BF data and result)."""
+    dt = torch.bfloat16 if bf16 else torch.float16
+    vdt = vk.DT_BF16 if bf16 else vk.DT_F16
     g = torch.Generator(device="cuda:0").manual_seed(7)
-    A = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).half()
-    B = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).half()
-    C = torch.empty(n * n, device="cuda:0", dtype=torch.float16)
+    A = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
+    B = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
+    C = torch.empty(n * n, device="cuda:0", dtype=dt)
     sp = stream.cuda_stream
     out = {}
     for name, ta in (("NN", 0), ("TN", 1)):
         def call():
-            vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
+            vk.gemm_async(vdt, vdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
                           C.data_ptr(), n, stream=sp)
         for _ in range(3):
             call()
@@ -126,18 +129,21 @@ def fp16_gemm(torch, vk, stream, steps, n=4096):
     return out
 
 
-def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16)):
+def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=False):
     """configs[3]: decode GemmEx(T, N, m=O, n=ntok, k=K), W K-contiguous;
-    three weight copies (3 x 128 MiB > 256 MB MALL) rotated per launch."""
+    three weight copies (3 x 128 MiB > 256 MB MALL) rotated per launch
+    (bf16: the same with 16BF data)."""
+    dt = torch.bfloat16 if bf16 else torch.float16
+    vdt = vk.DT_BF16 if bf16 else vk.DT_F16
     g = torch.Generator(device="cuda:0").manual_seed(11)
-    Ws = [(torch.randn(O * K, device="cuda:0", generator=g) * 0.02).half() for _ in range(3)]
-    X = torch.randn(16 * K, device="cuda:0", generator=g).half()
-    Y = torch.empty(16 * O, device="cuda:0", dtype=torch.float16)
+    Ws = [(torch.randn(O * K, device="cuda:0", generator=g) * 0.02).to(dt) for _ in range(3)]
+    X = torch.randn(16 * K, device="cuda:0", generator=g).to(dt)
+    Y = torch.empty(16 * O, device="cuda:0", dtype=dt)
     sp = stream.cuda_stream
     out = {}
     for nt in ntoks:
         def call(i):
-            vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_T, nt, O, K, 1.0, X.data_ptr(), K,
+            vk.gemm_async(vdt, vdt, vk.OP_N, vk.OP_T, nt, O, K, 1.0, X.data_ptr(), K,
                           Ws[i % 3].data_ptr(), K, 0.0, Y.data_ptr(), O, stream=sp)
         for i in range(6):
             call(i)
@@ -191,7 +197,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["fp32", "fp16", "matvec", "splitk", "batched", "calibrate"], default=None)
+    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "splitk", "batched", "calibrate"],
+                    default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -207,8 +214,14 @@ def main():
     if args.only == "fp16":
         print(json.dumps(fp16_gemm(torch, vk, stream, args.steps)))
         return
+    if args.only == "bf16":
+        print(json.dumps(fp16_gemm(torch, vk, stream, args.steps, bf16=True)))
+        return
     if args.only == "matvec":
         print(json.dumps(matvec(torch, vk, stream, args.steps)))
+        return
+    if args.only == "bf16mv":
+        print(json.dumps(matvec(torch, vk, stream, args.steps, bf16=True)))
         return
     if args.only == "splitk":
         print(json.dumps(splitk(torch, vk, stream, args.steps)))
@@ -260,6 +273,10 @@ def main():
     line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps)
     log("[bench] fp16 matvec 8192x8192")
     line["fp16_matvec_8192"] = matvec(torch, vk, stream, args.steps)
+    log("[bench] bf16 4096^3")
+    line["bf16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps, bf16=True)
+    log("[bench] bf16 matvec 8192x8192")
+    line["bf16_matvec_8192"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8), bf16=True)
     print(json.dumps(line), flush=True)
 
 

@@ -100,7 +100,9 @@ def test_engine_param_errors_without_gpu():
     p = 4096
     assert vk.gemm_f32(0, 0, 0, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
     assert vk.gemm_f16(0, 0, 4, 4, 4, 1.0, None, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
-    assert vk.load().vkblas_gemm_bf16(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, 1, 0, 0, 0) == vk.ERR_INIT
+    assert vk.gemm_bf16(0, 0, 4, 0, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
+    # valid arguments with no GPU in the process: initialisation fails loudly
+    assert vk.gemm_bf16(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_INIT
     for name in ("vkblas_gemm_c64", "vkblas_gemm_f64", "vkblas_gemm_z64"):
         assert hasattr(vk.load(), name)
 

@@ -181,7 +181,9 @@ def test_engine_rejects_bad_params():
     assert vk.gemm_f32(0, 0, 0, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
     assert vk.gemm_f32(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, 0) == vk.ERR_PARAM
     assert vk.gemm_f32(0, 0, 4, 4, 8, 1.0, p, 0, p, 4, 0.0, p, 4) == vk.ERR_PARAM   # lda == 0
-    assert vk.load().vkblas_gemm_bf16(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, 1, 0, 0, 0) == vk.ERR_INIT
+    assert vk.gemm_bf16(0, 0, 0, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4) == vk.ERR_PARAM
+    assert vk.gemm_bf16(0, 0, 4, 4, 4, 1.0, p, 4, p, 4, 0.0, p, 4, 0) == vk.ERR_PARAM
+    assert vk.gemm_bf16_hipblas(0, 0, 4, 4, 4, 1.0, p, 0, p, 4, 0.0, p, 4) == vk.ERR_PARAM
 
 
 def test_hipblas_zero_size_forwards():

@@ -9,8 +9,9 @@
   also meet the north-star bound: normwise relative error <= 2e-3.
 * test/test_v9h.c (hipblasGemmEx): 7 boundary cases x {bf16, fp16} with
   values +-[0.5,1) (test_v9h.c:63-128), bar max_rel < 0.02 with
-  rel = |got - acc| / (1 + |acc|).  fp16 runs on this library's kernels; bf16
-  is not on this build's path and exercises forwarding to the real hipBLAS.
+  rel = |got - acc| / (1 + |acc|).  Both types run on this library's kernels
+  (the reference routes 16BF GemmEx to its bf16 engine entry,
+  src/vkblas_hipblas.c:426-427).
 """
 import numpy as np
 import pytest

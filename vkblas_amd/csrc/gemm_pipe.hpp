@@ -346,13 +346,27 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     } else {
         region(0, 0, false, true, true);
         int kt = 1;
-        for (; kt + 3 < nkt; kt += 2) {
-            region(kt, 1, true, true, true);
-            region(kt + 1, 0, true, true, true);
+        if constexpr (SH == 0) {
+            // One region per iteration, stage from the loop counter: with two
+            // (stages 1 and 0 as constants) the register allocator gives the
+            // accumulator tiles different registers in the two halves and
+            // copies them around on every iteration (AGPR moves and parking
+            // in VGPRs, ~100 extra VALU per two K steps).  The other shapes
+            // keep the constant stages: their staged stores' addresses fold
+            // into immediates, and they show no such copies.
+#pragma clang loop unroll(disable)
+            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, true);
+            region(kt, kt & 1, true, true, false);             // kt == nkt - 2: loads step nkt-1
+            region(kt + 1, (kt + 1) & 1, true, false, false);
+        } else {
+            for (; kt + 3 < nkt; kt += 2) {
+                region(kt, 1, true, true, true);
+                region(kt + 1, 0, true, true, true);
+            }
+            region(kt, 1, true, true, true);       // kt == nkt - 3: stages step nkt-1
+            region(kt + 1, 0, true, true, false);  // loads step nkt-1
+            region(kt + 2, 1, true, false, false);
         }
-        region(kt, 1, true, true, true);       // kt == nkt - 3: stages step nkt-1
-        region(kt + 1, 0, true, true, false);  // loads step nkt-1
-        region(kt + 2, 1, true, false, false);
     }
 #pragma unroll
     for (int q = 0; q < UPS; ++q) mfma_unit((NSUB - 1) & 1, q);   // last sub-step of the last K step
