@@ -117,9 +117,12 @@ def test_plan_headline_configs():
     for n in (2048, 4096, 8192):
         assert P(vk.DT_F16, vk.DT_F16, 0, 0, n, n, n, n, n, n).path in (vk.PATH_TILE128, vk.PATH_TILE256)
     # config 4: decode (engine op_a = N, op_b = T, M = tokens)
-    for ntok in (1, 4, 8, 16):
-        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192)
-        assert pl.path == vk.PATH_SKINNY
+    for ntok in (1, 4, 8, 16, 17, 32, 64):
+        for dt in (vk.DT_F16, vk.DT_BF16):
+            pl = P(dt, dt, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192)
+            assert pl.path == vk.PATH_SKINNY
+    # 65 tokens: a GEMM again
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     # not skinny when misaligned, batched, or fp32
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, aligned=False).path != vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, batch=2).path != vk.PATH_SKINNY

@@ -1,5 +1,6 @@
-"""Edge cases of the decode kernels (engine op_a = N, op_b = T, M <= 16: the
-GEMV kernel for M <= 2, the MFMA skinny kernel above; fp16 and bf16), the path the
+"""Edge cases of the decode kernels (engine op_a = N, op_b = T, M <= 64: the
+GEMV kernel for M <= 2, the MFMA skinny kernel above, with up to four
+16-row activation tiles from M = 17; fp16 and bf16), the path the
 reference reaches for matvec / skinny shapes (src/vkblas.c:2100-2392,
 2501-2808).  Ragged K (not a multiple of the kernels' K steps), padded
 leading dimensions whose padding holds NaN (it must never reach C), beta != 0,
@@ -24,7 +25,15 @@ for M in (1, 2, 3, 4, 5, 8, 16):
 for M in (1, 2, 3, 8, 16):
     for (N, K) in ((7, 504), (1000, 1032), (300, 4104)):
         CASES.append((M, N, K, 0, 0, 0.0, "bf16"))
+for M in (17, 31, 32, 47, 64):
+    for (N, K) in ((7, 504), (1000, 1032), (300, 4104)):
+        CASES.append((M, N, K, 0, 0, 0.0, "f16"))
+    CASES.append((M, 520, 2056, 0, 0, 0.0, "bf16"))
 CASES += [
+    (20, 640, 1000, 8, 24, -0.5, "f16"),
+    (33, 333, 4104, 16, 8, 0.75, "f16>f32"),
+    (48, 1024, 2048, 0, 0, 0.25, "bf16>f32"),
+    (64, 777, 1032, 24, 0, 1.0, "bf16"),
     (1, 1000, 1032, 8, 16, 0.0, "f16"),
     (1, 777, 1000, 16, 8, 0.5, "bf16"),
     (5, 640, 2056, 8, 24, -0.5, "bf16"),
@@ -86,7 +95,7 @@ def test_decode_edges(case):
     assert normwise(g, w) <= (BF16_BOUND if bf and not f32 else F16_BOUND)
 
 
-@pytest.mark.parametrize("M", [1, 4, 12])
+@pytest.mark.parametrize("M", [1, 4, 12, 40])
 def test_decode_device_scalars(M):
     """alpha / beta in device memory (hipBLAS pointer mode device)."""
     import torch
@@ -114,7 +123,7 @@ def test_decode_deterministic():
     import vkblas_amd as vk
     from gpu_helpers import to_dev, to_host
     print("[case] decode determinism", flush=True)
-    for M in (1, 3, 9):
+    for M in (1, 3, 9, 40):
         N, K = 2048, 4096
         dX, dW = to_dev(_padded(M, K, K, 21, 1.0)), to_dev(_padded(N, K, K, 22, 0.05))
         outs = []

@@ -142,14 +142,14 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (lda == 0 || ldb == 0 || ldc == 0) return VKBLAS_ERR_PARAM;
     if (split_k == 0 && g_force_split) split_k = g_force_split;
 
-    /* decode-shaped fp16 / bf16: X[M<=16, K] . W[N, K]^T, both K-contiguous */
-    if ((ab_type == VKBLAS_DT_F16 || ab_type == VKBLAS_DT_BF16) && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 16 &&
+    /* decode-shaped fp16 / bf16: X[M<=64, K] . W[N, K]^T, both K-contiguous */
+    if ((ab_type == VKBLAS_DT_F16 || ab_type == VKBLAS_DT_BF16) && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 64 &&
         batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && lda >= K && ldb >= K &&
         !g_no_skinny) {
         plan->path = VKBLAS_PATH_SKINNY;
         plan->tile = VKB_TILE_64;
-        plan->split = 1;
-        plan->k_per_split = K;
+        plan->split = vkb_skinny_split(M, N, K);
+        plan->k_per_split = K;   /* the decode kernel splits whole K steps itself */
         return VKBLAS_OK;
     }
 
@@ -249,9 +249,23 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
                 path_name(plan.path), plan.split);
 
-    if (plan.path == VKBLAS_PATH_SKINNY) {
+    if (plan.path == VKBLAS_PATH_SKINNY && plan.split > 1) {
+        /* decode with K split over workgroups: fp32 partials, fixed-order reduce */
+        hipMemPool_t pool = pool_for_current_device();
+        if (!pool) return VKBLAS_ERR_INIT;
+        void* ws = NULL;
+        if (hipMallocFromPoolAsync(&ws, (size_t)plan.split * M * N * sizeof(float), pool, (hipStream_t)stream) !=
+            hipSuccess)
+            return VKBLAS_ERR_INIT;
+        rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode, alpha_dev,
+                               beta_dev, (float*)ws, plan.split, stream);
+        if (rc == 0)
+            rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
+                                          (int)scalar_mode, alpha_dev, beta_dev, stream);
+        hipFreeAsync(ws, (hipStream_t)stream);
+    } else if (plan.path == VKBLAS_PATH_SKINNY) {
         rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
-                                   alpha_dev, beta_dev, stream);
+                               alpha_dev, beta_dev, NULL, 1, stream);
     } else {
         vkb_gemm_args a;
         memset(&a, 0, sizeof(a));

@@ -8,7 +8,7 @@
 // (VKBLAS_CACHE_TRANSPOSE, src/vkblas.c:3543-3554, 1670-1691); here that layout
 // is the native one.
 //
-//   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n],  m < M <= 16
+//   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n],  m < M <= 64
 //
 // Work decomposition: a workgroup owns R tiles of 16 weight rows; its WAVES
 // waves split K into contiguous slices.  Per 128-wide K step a lane streams
@@ -60,6 +60,10 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float a) {
     else
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x), a, false);
 }
+
+// decode_kernel from this many activation rows on; weight tiles per wave
+constexpr int DEC_MIN_M = 17;
+constexpr int DEC_R = 2;
 
 struct SkParams {
     const uint16_t* X;   // 16-bit elements (fp16 or bf16 bit patterns)
@@ -355,6 +359,182 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
     }
 }
 
+// ------------------------------------------------------- shared-X decode
+// For M up to 64 activation rows.  In skinny_kernel each wave reads its own
+// activation fragments, so the activations are re-read from L2 once per
+// 16-32 weight rows: at M = 64 that is 2-4x the weight bytes.  Here the four
+// waves of a workgroup own different weight rows (wave w: rows 16 R w ..
+// 16 R w + 16 R - 1 of the workgroup's 64 R) and walk the same K steps; each
+// step's activation chunk (16 MT rows x 128 k) is loaded once per workgroup
+// into LDS and read by all four waves.  The grid is filled by splitting K
+// over blockIdx.y: with nsplit > 1 each workgroup writes raw fp32 partials
+// (part + split * M * N, row pitch N) that splitk_reduce sums in split order.
+//
+// LDS chunk layout: row r (activation row), 16-byte piece c (k 8c .. 8c+7)
+// at r * 16 + (c ^ (r & 15)) (u32x4 units).  The fragment reads (16 lanes:
+// rows r .. r+15, one piece) and the staging writes (16 threads: one row,
+// pieces 0 .. 15) then each cover all 64 banks.
+// Pipeline per K step c: load step c+D's activation chunk and then its
+// weights into a D-step register window, MFMAs of step c (activations from
+// LDS), write step c+1's chunk (loaded D-1 steps ago) to the other LDS
+// buffer, barrier.  Vector loads complete in issue order, so each wait covers
+// only the loads the step needs; everything issued later stays in flight.
+template <typename T, typename TC, int R, int MT, int D, bool PARTIAL>
+__global__ __launch_bounds__(256) void decode_kernel(SkParams p, float* part, int nsplit) {
+    __shared__ u32x4 xl[2][16 * MT * 16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int wrow0 = blockIdx.x * 64 * R + wave * 16 * R;     // this wave's first weight row
+    const int K = (int)p.K;
+    const int nsteps = (K + 127) / 128, full_steps = K / 128;
+    const int per = (nsteps + nsplit - 1) / nsplit;
+    const int s_beg = (int)blockIdx.y * per;
+    const int n = max(0, min(nsteps, s_beg + per) - s_beg);   // uniform over the workgroup
+
+    // Weight buffer on this wave's first row, activation buffer on X; the
+    // record counts are the read domains, so rows past N / M read as zero.
+    const int rows_here = min(16 * R, (int)p.N - wrow0);
+    const int w_records = rows_here > 0 ? (int)(((int64_t)(rows_here - 1) * p.ldb + K) * 2) : 0;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.W + (int64_t)max(0, min(wrow0, (int)p.N - 1)) * p.ldb), (short)0, w_records, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + K) * 2), 0x00020000);
+    int w_off[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) w_off[r] = (int)(((int64_t)(r * 16 + l16) * p.ldb + g * 8) * 2);
+    // staging: thread tid moves piece tid & 15 of rows tid / 16 + 16 i
+    const int srow = tid >> 4, spc = tid & 15;
+    int x_off[MT], x_lds[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int row = srow + 16 * i;
+        x_off[i] = (int)(((int64_t)row * p.lda + spc * 8) * 2);
+        x_lds[i] = row * 16 + (spc ^ (row & 15));
+    }
+    // fragment reads: row 16 t + l16, piece 4 j + g
+    int f_lds[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) f_lds[j] = l16 * 16 + ((4 * j + g) ^ l16);
+
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    auto stage_load = [&](int c, u32x4* xs) {
+        if (c < full_steps) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[i], c * 256, 0);
+        } else {   // partial last step: k >= K reads as zero
+#pragma unroll
+            for (int i = 0; i < MT; ++i) {
+                const int row = srow + 16 * i;
+                const int k = c * 128 + spc * 8;
+                xs[i] = row < (int)p.M ? ld8_checked(p.X + (int64_t)row * p.lda + k, K - k) : zero;
+            }
+        }
+    };
+    auto stage_store = [&](int b, const u32x4* xs) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) xl[b][x_lds[i]] = xs[i];
+    };
+    auto w_load = [&](int c, u32x4 (*wv)[4]) {
+        if (c < full_steps) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[r] + j * 64, c * 256, 0);
+        } else {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int row = wrow0 + r * 16 + l16;
+                    const int k = c * 128 + j * 32 + g * 8;
+                    wv[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, K - k) : zero;
+                }
+        }
+    };
+
+    floatx4 acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) acc[r][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    u32x4 wv[D][R][4], xs[D][MT];
+#pragma unroll
+    for (int s = 0; s < D; ++s)
+        if (s < n) {
+            stage_load(s_beg + s, xs[s]);
+            w_load(s_beg + s, wv[s]);
+        }
+    if (n > 0) stage_store(0, xs[0]);
+    __syncthreads();
+
+    for (int i0 = 0; i0 < n; i0 += D) {
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+            const int i = i0 + s;
+            if (i < n) {                       // uniform
+                const int c = s_beg + i, b = i & 1;
+                u32x4 xf[MT][4];
+#pragma unroll
+                for (int t = 0; t < MT; ++t)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) xf[t][j] = xl[b][t * 256 + f_lds[j]];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < R; ++r)
+#pragma unroll
+                        for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wv[s][r][j], xf[t][j], acc[r][t]);
+                // slot s is free again: step c+D's activations, then weights
+                if (i + D < n) {
+                    stage_load(c + D, xs[s]);
+                    w_load(c + D, wv[s]);
+                }
+                // step c+1's chunk (slot (s+1) % D) to the other buffer
+                if (i + 1 < n) stage_store(b ^ 1, xs[(s + 1) % D]);
+                // LDS traffic only: the loads in flight (registers of this
+                // wave) stay outstanding across the barrier
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+        }
+    }
+
+    // D row 4 g + e = weight row, column l16 = activation row: each lane
+    // holds four consecutive outputs of one activation row
+    float alpha = p.alpha, beta = p.beta;
+    if constexpr (!PARTIAL) {
+        if (p.mode == 1) {
+            alpha = *(const float*)p.alpha_dev;
+            beta = *(const float*)p.beta_dev;
+        } else if (p.mode == 2) {
+            alpha = (float)*(const _Float16*)p.alpha_dev;
+            beta = (float)*(const _Float16*)p.beta_dev;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const int row = 16 * t + l16;             // activation row (output row)
+            const int o = wrow0 + 16 * r + 4 * g;     // first of four weight rows (output columns)
+            if (row >= (int)p.M) continue;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (o + e >= (int)p.N) continue;
+                if constexpr (PARTIAL) {
+                    part[(int64_t)blockIdx.y * p.M * p.N + (int64_t)row * p.N + o + e] = acc[r][t][e];
+                } else {
+                    TC* dst = (TC*)p.C + (int64_t)row * p.ldc + o + e;
+                    float y = alpha * acc[r][t][e];
+                    if (beta != 0.0f) y += beta * (float)*dst;
+                    *dst = (TC)y;
+                }
+            }
+        }
+}
+
 template <typename T, typename TC, int MM, int RB>
 int launch_gemv(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + RB - 1) / RB;
@@ -369,20 +549,46 @@ int launch_sk(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
+// Shared-X decode: R weight tiles per wave (64 R rows per workgroup), MT
+// activation tiles, D K steps of weights in flight.
+template <typename T, typename TC, int R, int MT, int D>
+int launch_dec(const SkParams& p, float* part, int nsplit, hipStream_t st) {
+    const dim3 grid((p.N + 64 * R - 1) / (64 * R), (uint32_t)nsplit);
+    if (nsplit > 1)
+        hipLaunchKernelGGL((decode_kernel<T, float, R, MT, D, true>), grid, dim3(256), 0, st, p, part, nsplit);
+    else
+        hipLaunchKernelGGL((decode_kernel<T, TC, R, MT, D, false>), grid, dim3(256), 0, st, p, part, nsplit);
+    return (int)hipGetLastError();
+}
+
+template <typename T, typename TC>
+int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
+    switch ((p.M + 15) / 16) {
+        case 1: return launch_dec<T, TC, DEC_R, 1, 2>(p, part, nsplit, st);
+        case 2: return launch_dec<T, TC, DEC_R, 2, 2>(p, part, nsplit, st);
+        case 3: return launch_dec<T, TC, DEC_R, 3, 2>(p, part, nsplit, st);
+        default: return launch_dec<T, TC, DEC_R, 4, 2>(p, part, nsplit, st);
+    }
+}
+
 // One element type: output fp32 or the input type.
 //   M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best for
 //   4096-14336 rows); more activation rows multiply its VALU work and
-//   registers, and the MFMA kernel is faster from M = 3 on.
-//   M > 2: four waves split K with four steps in flight.  One 16-row tile per
-//   workgroup maximises workgroups; with more than 4 activation rows, two
-//   tiles share each activation load when that still leaves >= 256
-//   workgroups (one per CU).
+//   registers.
+//   3 <= M <= DEC_MIN_M - 1: skinny_kernel: four waves split K with four
+//   steps in flight.  One 16-row tile per workgroup maximises workgroups;
+//   with more than 4 activation rows, two tiles share each activation load
+//   when that still leaves >= 256 workgroups (one per CU).
+//   DEC_MIN_M <= M <= 64: decode_kernel (activations shared through LDS),
+//   K split nsplit ways over the grid.
 template <typename T>
-int launch_typed(const SkParams& p, bool f32_out, hipStream_t st) {
+int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipStream_t st) {
     if (p.M <= 2) {
         if (f32_out) return p.M == 1 ? launch_gemv<T, float, 1, 4>(p, st) : launch_gemv<T, float, 2, 4>(p, st);
         return p.M == 1 ? launch_gemv<T, T, 1, 4>(p, st) : launch_gemv<T, T, 2, 4>(p, st);
     }
+    if ((int)p.M >= DEC_MIN_M)
+        return f32_out ? launch_dec_mt<T, float>(p, part, nsplit, st) : launch_dec_mt<T, T>(p, part, nsplit, st);
     const bool two = p.M > 4 && (p.N + 31) / 32 >= 256;
     if (f32_out) return two ? launch_sk<T, float, 2, 4, 4>(p, st) : launch_sk<T, float, 1, 4, 4>(p, st);
     return two ? launch_sk<T, T, 2, 4, 4>(p, st) : launch_sk<T, T, 1, 4, 4>(p, st);
@@ -390,18 +596,34 @@ int launch_typed(const SkParams& p, bool f32_out, hipStream_t st) {
 
 }  // namespace
 
+extern "C" uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K) {
+    if ((int)M < DEC_MIN_M || M > 64) return 1;
+    // about two workgroups per CU, at least four K steps per slice
+    const uint32_t wg = (N + 64 * DEC_R - 1) / (64 * DEC_R);
+    const uint32_t nsteps = (K + 127) / 128;
+    uint32_t split = (512 + wg - 1) / wg;
+    if (split > nsteps / 4) split = nsteps / 4;
+    if (split < 1) split = 1;
+    // every slice non-empty
+    const uint32_t per = (nsteps + split - 1) / split;
+    return (nsteps + per - 1) / per;
+}
+
 extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
                                  void* C, int64_t ldc, int c_type,
                                  uint32_t M, uint32_t N, uint32_t K,
                                  float alpha, float beta, int scalar_mode,
-                                 const void* alpha_dev, const void* beta_dev, void* stream) {
-    if (M == 0 || M > 16 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
+                                 const void* alpha_dev, const void* beta_dev,
+                                 float* part, uint32_t nsplit, void* stream) {
+    if (M == 0 || M > 64 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
     if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) return (int)hipErrorInvalidValue;
     if (c_type != VKB_T_F32 && c_type != ab_type) return (int)hipErrorInvalidValue;
     if ((lda & 7) || (ldb & 7) || ((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
-    // buffer offsets are 32-bit: a 32-row weight tile and the activations
-    // must span less than 2 GiB
-    if ((uint64_t)32 * ldb * 2 >= (1ull << 31) || (uint64_t)M * lda * 2 >= (1ull << 31)) return (int)hipErrorInvalidValue;
+    if (nsplit != vkb_skinny_split(M, N, K) || (nsplit > 1 && !part)) return (int)hipErrorInvalidValue;
+    // buffer offsets are 32-bit: a 32-row weight tile and the activation
+    // tiles (rows up to 16 ceil(M / 16)) must span less than 2 GiB
+    const uint64_t xrows = M <= 16 ? M : 16 * ((M + 15) / 16);
+    if ((uint64_t)32 * ldb * 2 >= (1ull << 31) || xrows * lda * 2 >= (1ull << 31)) return (int)hipErrorInvalidValue;
     SkParams p;
     p.X = (const uint16_t*)X; p.W = (const uint16_t*)W; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
@@ -410,5 +632,6 @@ extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const 
     p.alpha_dev = alpha_dev; p.beta_dev = beta_dev;
     hipStream_t st = (hipStream_t)stream;
     const bool f32_out = c_type == VKB_T_F32;
-    return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, st) : launch_typed<_Float16>(p, f32_out, st);
+    return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, part, (int)nsplit, st)
+                                 : launch_typed<_Float16>(p, f32_out, part, (int)nsplit, st);
 }

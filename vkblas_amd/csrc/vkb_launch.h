@@ -74,16 +74,20 @@ int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t spli
                              float alpha, float beta, int scalar_mode,
                              const void* alpha_dev, const void* beta_dev, void* stream);
 
-/* Skinny 16-bit GEMM for decode (M <= 16 rows of activations):
+/* Skinny 16-bit GEMM for decode (M <= 64 rows of activations):
  *   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n]
  * X = A (K-contiguous rows, lda), W = B (K-contiguous rows, ldb); ab_type F16
  * or BF16, c_type F32 or ab_type.  Requires lda, ldb multiples of 8 and
- * 16-byte aligned A, B. */
+ * 16-byte aligned A, B.  nsplit must be vkb_skinny_split(M, N, K); when it
+ * is > 1 the kernel writes fp32 partials to part ([nsplit][M][N], row pitch
+ * N) and the caller finishes with vkb_launch_splitk_reduce. */
+uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K);
 int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
                       void* C, int64_t ldc, int c_type,
                       uint32_t M, uint32_t N, uint32_t K,
                       float alpha, float beta, int scalar_mode,
-                      const void* alpha_dev, const void* beta_dev, void* stream);
+                      const void* alpha_dev, const void* beta_dev,
+                      float* part, uint32_t nsplit, void* stream);
 
 #ifdef __cplusplus
 }
