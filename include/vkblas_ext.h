@@ -67,6 +67,29 @@ vkblas_status_t vkblas_gemm_async(
     uint32_t split_k,
     void* stream);
 
+/*
+ * Pointer-array batched GEMM on a HIP stream: A, B, C are device arrays of
+ * `batch` matrix pointers (hipblas*gemmBatched), each matrix with the same
+ * shape, op and leading dimension; batch b computes
+ *   C[b] = alpha * op(A[b]) op(B[b]) + beta * C[b]   (row-major engine contract).
+ * Type combinations, scalars and status as vkblas_gemm_async.  The matrices
+ * need no particular alignment.  Never split-K or the skinny path (their
+ * planning needs the matrix pointers on the host).  No reference counterpart:
+ * the reference forwards pointer-array batched calls to the vendor library.
+ */
+vkblas_status_t vkblas_gemm_batched_async(
+    vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+    vkblas_op_t op_a, vkblas_op_t op_b,
+    uint32_t M, uint32_t N, uint32_t K,
+    float alpha,
+    const void* const* A, uint32_t lda,
+    const void* const* B, uint32_t ldb,
+    float beta,
+    void* const* C, uint32_t ldc,
+    uint32_t batch,
+    vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
+    void* stream);
+
 /* The path planned for a call with these arguments (no GPU needed).
  * aligned: A, B, C base pointers 16-byte aligned (the skinny kernel needs it).
  * Returns VKBLAS_OK or VKBLAS_ERR_PARAM. */

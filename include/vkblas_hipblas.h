@@ -6,7 +6,8 @@
  * (ROCm 7.2); the shim includes this header next to <hipblas/hipblas.h>, so
  * the compiler checks every declaration here against the vendor's.
  *
- * Computed by this library (gfx950 kernels): Sgemm*, Hgemm*, and GemmEx* with
+ * Computed by this library (gfx950 kernels): Sgemm*, Hgemm*, and GemmEx* (plain,
+ * strided-batched and pointer-array batched) with
  * fp32 data, fp16 data (fp16 or fp32 result) and bf16 data (bf16 or fp32
  * result).  Forwarded to the real hipBLAS when declined (degenerate sizes,
  * other types).
@@ -243,6 +244,39 @@ VKBLAS_FOUR(VKBLAS_GELS_DECL, SgelsBatched, DgelsBatched, CgelsBatched, ZgelsBat
 VKBLAS_FOUR(VKBLAS_GEQRF_DECL, SgeqrfBatched, DgeqrfBatched, CgeqrfBatched, ZgeqrfBatched)
 VKBLAS_FOUR(VKBLAS_GETRF_DECL, SgetrfBatched, DgetrfBatched, CgetrfBatched, ZgetrfBatched)
 VKBLAS_FOUR(VKBLAS_GETRS_DECL, SgetrsBatched, DgetrsBatched, CgetrsBatched, ZgetrsBatched)
+
+/* Pointer-array batched GEMMs: no counterpart in the reference, which left
+ * them to the real hipBLAS.  A, B, C are device arrays of batchCount matrix
+ * pointers; computed for the same types as the non-batched entries. */
+hipblasStatus_t hipblasSgemmBatched(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                    int m, int n, int k, const float* alpha, const float* const AP[], int lda,
+                                    const float* const BP[], int ldb, const float* beta, float* const CP[], int ldc,
+                                    int batchCount);
+hipblasStatus_t hipblasSgemmBatched_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                       hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                       const float* alpha, const float* const AP[], int64_t lda,
+                                       const float* const BP[], int64_t ldb, const float* beta, float* const CP[],
+                                       int64_t ldc, int64_t batchCount);
+hipblasStatus_t hipblasHgemmBatched(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                    int m, int n, int k, const hipblasHalf* alpha, const hipblasHalf* const AP[],
+                                    int lda, const hipblasHalf* const BP[], int ldb, const hipblasHalf* beta,
+                                    hipblasHalf* const CP[], int ldc, int batchCount);
+hipblasStatus_t hipblasHgemmBatched_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                       hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                       const hipblasHalf* alpha, const hipblasHalf* const AP[], int64_t lda,
+                                       const hipblasHalf* const BP[], int64_t ldb, const hipblasHalf* beta,
+                                       hipblasHalf* const CP[], int64_t ldc, int64_t batchCount);
+hipblasStatus_t hipblasGemmBatchedEx(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                     int m, int n, int k, const void* alpha, const void* A[], hipDataType aType,
+                                     int lda, const void* B[], hipDataType bType, int ldb, const void* beta,
+                                     void* C[], hipDataType cType, int ldc, int batchCount,
+                                     hipblasComputeType_t computeType, hipblasGemmAlgo_t algo);
+hipblasStatus_t hipblasGemmBatchedEx_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                        hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                        const void* alpha, const void* A[], hipDataType aType, int64_t lda,
+                                        const void* B[], hipDataType bType, int64_t ldb, const void* beta,
+                                        void* C[], hipDataType cType, int64_t ldc, int64_t batchCount,
+                                        hipblasComputeType_t computeType, hipblasGemmAlgo_t algo);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,24 @@ rocblas_status(rocblas_gemm_strided_batched_ex_64)(
     rocblas_datatype d_type, int64_t ldd, rocblas_stride stride_d, int64_t batch_count,
     rocblas_datatype compute_type, rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags);
 
+/* Pointer-array batched: no counterpart in the reference, which forwarded it.
+ * a, b, c, d are device arrays of batch_count matrix pointers; D must be C. */
+rocblas_status(rocblas_gemm_batched_ex)(rocblas_handle handle, rocblas_operation transA, rocblas_operation transB,
+                                        rocblas_int m, rocblas_int n, rocblas_int k, const void* alpha,
+                                        const void* a, rocblas_datatype a_type, rocblas_int lda, const void* b,
+                                        rocblas_datatype b_type, rocblas_int ldb, const void* beta, const void* c,
+                                        rocblas_datatype c_type, rocblas_int ldc, void* d, rocblas_datatype d_type,
+                                        rocblas_int ldd, rocblas_int batch_count, rocblas_datatype compute_type,
+                                        rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags);
+rocblas_status(rocblas_gemm_batched_ex_64)(rocblas_handle handle, rocblas_operation transA,
+                                           rocblas_operation transB, int64_t m, int64_t n, int64_t k,
+                                           const void* alpha, const void* a, rocblas_datatype a_type, int64_t lda,
+                                           const void* b, rocblas_datatype b_type, int64_t ldb, const void* beta,
+                                           const void* c, rocblas_datatype c_type, int64_t ldc, void* d,
+                                           rocblas_datatype d_type, int64_t ldd, int64_t batch_count,
+                                           rocblas_datatype compute_type, rocblas_gemm_algo algo,
+                                           int32_t solution_index, uint32_t flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,9 @@ class RocblasHandle:
         L.rocblas_gemm_strided_batched_ex.argtypes = [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i64, _vp, _i, _i,
                                                       _i64, _vp, _vp, _i, _i, _i64, _vp, _i, _i, _i64, _i, _i, _i,
                                                       ctypes.c_int32, _u32]
+        L.rocblas_gemm_batched_ex.restype = _i
+        L.rocblas_gemm_batched_ex.argtypes = [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _vp, _i,
+                                              _i, _vp, _i, _i, _i, _i, _i, ctypes.c_int32, _u32]
 
     def set_stream(self, s):
         assert self.real.rocblas_set_stream(self.h, _vp(s)) == 0
@@ -257,3 +260,34 @@ def test_forwarded_calls_still_work(rh):
     st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], 0, n, k, fbox(1.0), b.data_ptr(), F16, n, a.data_ptr(), F16,
                                 k, fbox(0.0), c.data_ptr(), F16, n, c.data_ptr(), F16, n, F32, 0, 0, 0)
     assert st == 0
+
+
+@pytest.mark.parametrize("dt", [F16, BF16])
+def test_gemm_batched_ex_ptr_array(rh, dt):
+    """rocblas_gemm_batched_ex: device arrays of matrix pointers (D == C computed here)."""
+    import torch
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, BF16_BOUND, fbox
+    m, n, k, nb = 120, 72, 88, 3
+    print(f"[case] rocblas_gemm_batched_ex {dt}", flush=True)
+    conv = oracle.f2bf_rne if dt == BF16 else oracle.f2h_rne
+    dec = oracle.bf2f if dt == BF16 else oracle.h2f
+    ref = oracle.ref_gemm_bf16_rm if dt == BF16 else oracle.ref_gemm_f16_rm
+    r = np.random.default_rng(31)
+    As = [conv((r.standard_normal(m * k) / 8).astype(np.float32)) for _ in range(nb)]
+    Bs = [conv(r.standard_normal(k * n).astype(np.float32)) for _ in range(nb)]
+    Cs = [conv(r.standard_normal(m * n).astype(np.float32)) for _ in range(nb)]
+    dA = [to_dev(a) for a in As]
+    dB = [to_dev(b) for b in Bs]
+    dC = [to_dev(c) for c in Cs]
+    pa = torch.tensor([t.data_ptr() for t in dA], dtype=torch.int64, device="cuda:0")
+    pb = torch.tensor([t.data_ptr() for t in dB], dtype=torch.int64, device="cuda:0")
+    pc = torch.tensor([t.data_ptr() for t in dC], dtype=torch.int64, device="cuda:0")
+    st = rh.lib.rocblas_gemm_batched_ex(rh.h, OP[0], OP[1], m, n, k, fbox(1.0), pa.data_ptr(), dt, m, pb.data_ptr(),
+                                        dt, n, fbox(0.5), pc.data_ptr(), dt, m, pc.data_ptr(), dt, m, nb, F32, 0, 0, 0)
+    assert st == 0
+    bound = BF16_BOUND if dt == BF16 else F16_BOUND
+    for i in range(nb):
+        want = Cs[i].copy()
+        # column-major C = A op(B)^T with B (n x k) -> engine: op_a = transB = T, op_b = transA = N
+        ref(1, 0, n, m, k, Bs[i], n, As[i], m, 1.0, 0.5, want, m)
+        assert normwise(dec(to_host(dC[i])), dec(want)) <= bound

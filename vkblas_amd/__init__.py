@@ -74,6 +74,9 @@ def load():
     L.vkblas_gemm_async.argtypes = [_int, _int, _int, _int, _u32, _u32, _u32, _f, _vp, _u32, _vp, _u32, _f, _vp,
                                     _u32, _u32, _i64, _i64, _i64, _int, _vp, _vp, _u32, _vp]
     L.vkblas_gemm_async.restype = _int
+    L.vkblas_gemm_batched_async.argtypes = [_int, _int, _int, _int, _u32, _u32, _u32, _f, _vp, _u32, _vp, _u32, _f,
+                                            _vp, _u32, _u32, _int, _vp, _vp, _vp]
+    L.vkblas_gemm_batched_async.restype = _int
     L.vkblas_plan_gemm.argtypes = [_int, _int, _int, _int, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _u32, _int,
                                    ctypes.POINTER(Plan)]
     L.vkblas_plan_gemm.restype = _int
@@ -121,6 +124,17 @@ def gemm_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta
                                   stream)
     if check and st != OK:
         raise VkblasError(st, "vkblas_gemm_async")
+    return st
+
+
+def gemm_batched_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch,
+                       scalar_mode=SCALAR_HOST, alpha_dev=None, beta_dev=None, stream=None, check=True) -> int:
+    """vkblas_gemm_batched_async: A, B, C are device addresses of arrays of
+    `batch` matrix pointers (pointer-array batched GEMM)."""
+    st = load().vkblas_gemm_batched_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
+                                          batch, scalar_mode, alpha_dev, beta_dev, stream)
+    if check and st != OK:
+        raise VkblasError(st, "vkblas_gemm_batched_async")
     return st
 
 

@@ -317,6 +317,59 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     return VKBLAS_OK;
 }
 
+vkblas_status_t vkblas_gemm_batched_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+                                          vkblas_op_t op_a, vkblas_op_t op_b,
+                                          uint32_t M, uint32_t N, uint32_t K,
+                                          float alpha,
+                                          const void* const* A, uint32_t lda,
+                                          const void* const* B, uint32_t ldb,
+                                          float beta,
+                                          void* const* C, uint32_t ldc,
+                                          uint32_t batch,
+                                          vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
+                                          const void* beta_dev, void* stream) {
+    if (!A || !B || !C) return VKBLAS_ERR_PARAM;
+    if (scalar_mode != VKBLAS_SCALAR_HOST && (!alpha_dev || !beta_dev)) return VKBLAS_ERR_PARAM;
+    if (scalar_mode != VKBLAS_SCALAR_HOST && scalar_mode != VKBLAS_SCALAR_DEV_F32 &&
+        scalar_mode != VKBLAS_SCALAR_DEV_F16)
+        return VKBLAS_ERR_PARAM;
+    /* split_k = 1 and aligned = 0: a tile path (no split, no skinny) */
+    vkblas_plan_t plan;
+    vkblas_status_t st = vkblas_plan_gemm(ab_type, c_type, op_a, op_b, M, N, K, lda, ldb, ldc, batch, 1, 0, &plan);
+    if (st != VKBLAS_OK) return st;
+    if (plan.path == VKBLAS_PATH_SPLITK || plan.path == VKBLAS_PATH_SKINNY) return VKBLAS_ERR_PARAM;
+    if (!ensure_init()) return VKBLAS_ERR_INIT;
+    const int ab = kernel_type(ab_type);
+    const int ct = kernel_type(c_type);
+    if (g_trace)
+        fprintf(stderr, "[vkblas] gemm batched %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s\n",
+                op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
+                path_name(plan.path));
+    vkb_gemm_args a;
+    memset(&a, 0, sizeof(a));
+    a.A = (const void*)A; a.B = (const void*)B; a.C = (void*)C;
+    a.lda = lda; a.ldb = ldb; a.ldc = ldc;
+    a.M = M; a.N = N; a.K = K;
+    a.batch = batch;
+    a.split = 1;
+    a.k_per_split = K;
+    a.a_kmajor = op_a == VKBLAS_OP_N;
+    a.b_kmajor = op_b == VKBLAS_OP_T;
+    a.ab_type = ab;
+    a.c_type = ct;
+    a.alpha = alpha; a.beta = beta;
+    a.scalar_mode = (int)scalar_mode;
+    a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
+    a.ptr_array = 1;
+    const int rc = vkb_launch_gemm(&a, plan.tile, stream);
+    if (rc != 0) {
+        if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s\n", hipGetErrorString((hipError_t)rc));
+        return VKBLAS_ERR_INIT;
+    }
+    g_last_path = plan.path;
+    return VKBLAS_OK;
+}
+
 int vkblas_last_path(void) { return g_last_path; }
 
 vkblas_status_t vkblas_set_override(int tile, int generic) {

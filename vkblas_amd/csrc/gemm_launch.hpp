@@ -61,13 +61,23 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     p.scalar_mode = a->scalar_mode;
     p.alpha_dev = a->alpha_dev; p.beta_dev = a->beta_dev;
     const bool multi = p.batch > 1;
-    p.vec_a = (a->lda % VEC == 0) && aligned(a->A, 16) && (!multi || a->stride_a % VEC == 0);
-    p.vec_b = (a->ldb % VEC == 0) && aligned(a->B, 16) && (!multi || a->stride_b % VEC == 0);
-    p.vec_c = (a->ldc % 4 == 0) && aligned(a->C, 4 * sizeof(TC)) && (!multi || a->stride_c % 4 == 0) &&
-              (p.split == 1 || p.s_split % 4 == 0);
+    p.ptr_array = a->ptr_array != 0;
+    if (p.ptr_array) {
+        // the matrices' alignment is checked per batch in the kernel, which
+        // always runs the checked instantiation (no pipelined kernel)
+        if (p.split > 1) return (int)hipErrorInvalidValue;
+        p.vec_a = a->lda % VEC == 0;
+        p.vec_b = a->ldb % VEC == 0;
+        p.vec_c = a->ldc % 4 == 0;
+    } else {
+        p.vec_a = (a->lda % VEC == 0) && aligned(a->A, 16) && (!multi || a->stride_a % VEC == 0);
+        p.vec_b = (a->ldb % VEC == 0) && aligned(a->B, 16) && (!multi || a->stride_b % VEC == 0);
+        p.vec_c = (a->ldc % 4 == 0) && aligned(a->C, 4 * sizeof(TC)) && (!multi || a->stride_c % 4 == 0) &&
+                  (p.split == 1 || p.s_split % 4 == 0);
+    }
     if (p.split > 1 && (p.kps == 0 || p.kps % BK != 0)) return (int)hipErrorInvalidValue;
 
-    const bool full = (a->M % bm == 0) && (a->N % bn == 0) && (a->K % BK == 0) &&
+    const bool full = !p.ptr_array && (a->M % bm == 0) && (a->N % bn == 0) && (a->K % BK == 0) &&
                       p.vec_a && p.vec_b && p.vec_c;
     const uint64_t grid64 = (uint64_t)p.tiles_m * p.tiles_n * p.batch * p.split;
     if (grid64 == 0 || grid64 > 0x7fffffffull) return (int)hipErrorInvalidValue;

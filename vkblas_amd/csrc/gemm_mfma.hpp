@@ -56,6 +56,10 @@ struct KParams {
     const void* beta_dev;
     int scalar_mode;
     int vec_a, vec_b, vec_c;
+    // A, B, C are device arrays of `batch` matrix pointers (the sa / sb / sc
+    // strides are unused); vec_* then also need each matrix aligned, which
+    // the kernel checks per batch
+    int ptr_array;
 };
 
 template <typename T> struct Elem;
@@ -306,9 +310,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
     const int m0 = (int)(first_m + tin % gm) * BM;
     const int n0 = (int)(tin / gm) * BN;
 
-    const T* Ab = (const T*)p.A + (int64_t)b * p.sa;
-    const T* Bb = (const T*)p.B + (int64_t)b * p.sb;
-    TC* Cb = (TC*)p.C + (int64_t)b * p.sc + (int64_t)s * p.s_split;
+    const T* Ab;
+    const T* Bb;
+    TC* Cb;
+    bool va = p.vec_a != 0, vb = p.vec_b != 0, vc = p.vec_c != 0;
+    if (p.ptr_array) {
+        Ab = ((const T* const*)p.A)[b];
+        Bb = ((const T* const*)p.B)[b];
+        Cb = ((TC* const*)p.C)[b];
+        va = va && ((uintptr_t)Ab & 15) == 0;
+        vb = vb && ((uintptr_t)Bb & 15) == 0;
+        vc = vc && ((uintptr_t)Cb & (4 * sizeof(TC) - 1)) == 0;
+    } else {
+        Ab = (const T*)p.A + (int64_t)b * p.sa;
+        Bb = (const T*)p.B + (int64_t)b * p.sb;
+        Cb = (TC*)p.C + (int64_t)b * p.sc + (int64_t)s * p.s_split;
+    }
     const int kbeg = (int)(s * p.kps);
     const int kend = (int)min((uint32_t)p.K, s * p.kps + p.kps);
     const int nkt = (kend - kbeg + BK - 1) / BK;
@@ -324,7 +341,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const bool va = p.vec_a != 0, vb = p.vec_b != 0;
     if (nkt > 0) {
         sa.load(Ab, p.lda, m0, (int)p.M, kbeg, kend, va, tid);
         sb.load(Bb, p.ldb, n0, (int)p.N, kbeg, kend, vb, tid);
@@ -407,7 +423,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
     // ---- epilogue: C[m][n..n+3] = alpha * acc + beta * C ----
     float alpha, beta;
     load_scalars(p, alpha, beta);
-    const bool vc = p.vec_c != 0;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int m = m0 + wm * WTM + i * 32 + l32;

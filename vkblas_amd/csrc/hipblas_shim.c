@@ -182,12 +182,14 @@ static const char* dtype_name(vkblas_dtype_t t) {
     return t == VKBLAS_DT_F16 ? "f16" : t == VKBLAS_DT_BF16 ? "bf16" : "f32";
 }
 
-static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkblas_dtype_t ct, int scal_f16,
-                                hipblasOperation_t transA, hipblasOperation_t transB,
-                                int64_t m, int64_t n, int64_t k, const void* alpha,
-                                const void* A, int64_t lda, int64_t sA,
-                                const void* B, int64_t ldb, int64_t sB, const void* beta,
-                                void* C, int64_t ldc, int64_t sC, int64_t batch) {
+/* ptr_array: A, B, C are device arrays of batch matrix pointers
+ * (hipblas*gemmBatched); the strides are then unused. */
+static hipblasStatus_t run_gemm_any(hipblasHandle_t handle, vkblas_dtype_t ab, vkblas_dtype_t ct, int scal_f16,
+                                    hipblasOperation_t transA, hipblasOperation_t transB,
+                                    int64_t m, int64_t n, int64_t k, const void* alpha,
+                                    const void* A, int64_t lda, int64_t sA,
+                                    const void* B, int64_t ldb, int64_t sB, const void* beta,
+                                    void* C, int64_t ldc, int64_t sC, int64_t batch, int ptr_array) {
     pthread_once(&g_real_once, real_open);
     if (m <= 0 || n <= 0 || k <= 0 || batch <= 0) return VKB_DECLINE;
     if (m > UINT32_MAX || n > UINT32_MAX || k > UINT32_MAX || batch > UINT32_MAX) return VKB_DECLINE;
@@ -227,19 +229,46 @@ static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkbla
         b = *(const float*)beta;
     }
     if (g_trace)
-        fprintf(stderr, "[vkblas] hipblas gemm %s%s %s->%s m=%lld n=%lld k=%lld lda=%lld ldb=%lld ldc=%lld batch=%lld\n",
-                op_is_t(transA) ? "T" : "N", op_is_t(transB) ? "T" : "N", dtype_name(ab), dtype_name(ct),
-                (long long)m, (long long)n, (long long)k, (long long)lda,
+        fprintf(stderr, "[vkblas] hipblas gemm%s %s%s %s->%s m=%lld n=%lld k=%lld lda=%lld ldb=%lld ldc=%lld "
+                        "batch=%lld\n",
+                ptr_array ? " batched" : "", op_is_t(transA) ? "T" : "N", op_is_t(transB) ? "T" : "N",
+                dtype_name(ab), dtype_name(ct), (long long)m, (long long)n, (long long)k, (long long)lda,
                 (long long)ldb, (long long)ldc, (long long)batch);
-    vkblas_status_t st = vkblas_gemm_async(
-        ab, ct, op_is_t(transB) ? VKBLAS_OP_T : VKBLAS_OP_N, op_is_t(transA) ? VKBLAS_OP_T : VKBLAS_OP_N,
-        (uint32_t)n, (uint32_t)m, (uint32_t)k, a, B, (uint32_t)ldb, A, (uint32_t)lda, b, C, (uint32_t)ldc,
-        (uint32_t)batch, batch > 1 ? sB : 0, batch > 1 ? sA : 0, batch > 1 ? sC : 0, sm, ad, bd, 0, stream);
+    const vkblas_op_t op_a = op_is_t(transB) ? VKBLAS_OP_T : VKBLAS_OP_N;
+    const vkblas_op_t op_b = op_is_t(transA) ? VKBLAS_OP_T : VKBLAS_OP_N;
+    vkblas_status_t st;
+    if (ptr_array)
+        st = vkblas_gemm_batched_async(ab, ct, op_a, op_b, (uint32_t)n, (uint32_t)m, (uint32_t)k, a,
+                                       (const void* const*)B, (uint32_t)ldb, (const void* const*)A, (uint32_t)lda,
+                                       b, (void* const*)C, (uint32_t)ldc, (uint32_t)batch, sm, ad, bd, stream);
+    else
+        st = vkblas_gemm_async(ab, ct, op_a, op_b, (uint32_t)n, (uint32_t)m, (uint32_t)k, a, B, (uint32_t)ldb, A,
+                               (uint32_t)lda, b, C, (uint32_t)ldc, (uint32_t)batch, batch > 1 ? sB : 0,
+                               batch > 1 ? sA : 0, batch > 1 ? sC : 0, sm, ad, bd, 0, stream);
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return VKB_DECLINE;
     }
     return HIPBLAS_STATUS_SUCCESS;
+}
+
+static hipblasStatus_t run_gemm(hipblasHandle_t handle, vkblas_dtype_t ab, vkblas_dtype_t ct, int scal_f16,
+                                hipblasOperation_t transA, hipblasOperation_t transB,
+                                int64_t m, int64_t n, int64_t k, const void* alpha,
+                                const void* A, int64_t lda, int64_t sA,
+                                const void* B, int64_t ldb, int64_t sB, const void* beta,
+                                void* C, int64_t ldc, int64_t sC, int64_t batch) {
+    return run_gemm_any(handle, ab, ct, scal_f16, transA, transB, m, n, k, alpha, A, lda, sA, B, ldb, sB, beta, C,
+                        ldc, sC, batch, 0);
+}
+
+static hipblasStatus_t run_gemm_batched(hipblasHandle_t handle, vkblas_dtype_t ab, vkblas_dtype_t ct, int scal_f16,
+                                        hipblasOperation_t transA, hipblasOperation_t transB,
+                                        int64_t m, int64_t n, int64_t k, const void* alpha,
+                                        const void* A, int64_t lda, const void* B, int64_t ldb, const void* beta,
+                                        void* C, int64_t ldc, int64_t batch) {
+    return run_gemm_any(handle, ab, ct, scal_f16, transA, transB, m, n, k, alpha, A, lda, 0, B, ldb, 0, beta, C,
+                        ldc, 0, batch, 1);
 }
 
 /* Data / compute type classification.  Values of the pre-3.0
@@ -551,6 +580,114 @@ hipblasStatus_t hipblasGemmStridedBatchedEx_64(hipblasHandle_t handle, hipblasOp
                hipblasComputeType_t, hipblasGemmAlgo_t),
               (handle, transA, transB, m, n, k, alpha, A, aType, lda, strideA, B, bType, ldb, strideB, beta, C,
                cType, ldc, strideC, batchCount, computeType, algo));
+}
+
+/* -------------------------------------------- pointer-array batched */
+/* No reference counterpart: the reference left these to the real hipBLAS.
+ * A, B, C are device arrays of batchCount matrix pointers. */
+
+hipblasStatus_t hipblasSgemmBatched(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                    int m, int n, int k, const float* alpha, const float* const AP[], int lda,
+                                    const float* const BP[], int ldb, const float* beta, float* const CP[], int ldc,
+                                    int batchCount) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    hipblasStatus_t s = run_gemm_batched(handle, VKBLAS_DT_F32, VKBLAS_DT_F32, 0, transA, transB, m, n, k, alpha,
+                                         AP, lda, BP, ldb, beta, (void*)CP, ldc, batchCount);
+    if (s != VKB_DECLINE) return s;
+    REAL_CALL(hipblasStatus_t, hipblasSgemmBatched,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int, int, int, const float*,
+               const float* const*, int, const float* const*, int, const float*, float* const*, int, int),
+              (handle, transA, transB, m, n, k, alpha, AP, lda, BP, ldb, beta, CP, ldc, batchCount));
+}
+
+hipblasStatus_t hipblasSgemmBatched_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                       hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                       const float* alpha, const float* const AP[], int64_t lda,
+                                       const float* const BP[], int64_t ldb, const float* beta, float* const CP[],
+                                       int64_t ldc, int64_t batchCount) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    hipblasStatus_t s = run_gemm_batched(handle, VKBLAS_DT_F32, VKBLAS_DT_F32, 0, transA, transB, m, n, k, alpha,
+                                         AP, lda, BP, ldb, beta, (void*)CP, ldc, batchCount);
+    if (s != VKB_DECLINE) return s;
+    REAL_CALL(hipblasStatus_t, hipblasSgemmBatched_64,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int64_t, int64_t, int64_t, const float*,
+               const float* const*, int64_t, const float* const*, int64_t, const float*, float* const*, int64_t,
+               int64_t),
+              (handle, transA, transB, m, n, k, alpha, AP, lda, BP, ldb, beta, CP, ldc, batchCount));
+}
+
+hipblasStatus_t hipblasHgemmBatched(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                    int m, int n, int k, const hipblasHalf* alpha, const hipblasHalf* const AP[],
+                                    int lda, const hipblasHalf* const BP[], int ldb, const hipblasHalf* beta,
+                                    hipblasHalf* const CP[], int ldc, int batchCount) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    hipblasStatus_t s = run_gemm_batched(handle, VKBLAS_DT_F16, VKBLAS_DT_F16, 1, transA, transB, m, n, k, alpha,
+                                         AP, lda, BP, ldb, beta, (void*)CP, ldc, batchCount);
+    if (s != VKB_DECLINE) return s;
+    REAL_CALL(hipblasStatus_t, hipblasHgemmBatched,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int, int, int, const hipblasHalf*,
+               const hipblasHalf* const*, int, const hipblasHalf* const*, int, const hipblasHalf*,
+               hipblasHalf* const*, int, int),
+              (handle, transA, transB, m, n, k, alpha, AP, lda, BP, ldb, beta, CP, ldc, batchCount));
+}
+
+hipblasStatus_t hipblasHgemmBatched_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                       hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                       const hipblasHalf* alpha, const hipblasHalf* const AP[], int64_t lda,
+                                       const hipblasHalf* const BP[], int64_t ldb, const hipblasHalf* beta,
+                                       hipblasHalf* const CP[], int64_t ldc, int64_t batchCount) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    hipblasStatus_t s = run_gemm_batched(handle, VKBLAS_DT_F16, VKBLAS_DT_F16, 1, transA, transB, m, n, k, alpha,
+                                         AP, lda, BP, ldb, beta, (void*)CP, ldc, batchCount);
+    if (s != VKB_DECLINE) return s;
+    REAL_CALL(hipblasStatus_t, hipblasHgemmBatched_64,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int64_t, int64_t, int64_t,
+               const hipblasHalf*, const hipblasHalf* const*, int64_t, const hipblasHalf* const*, int64_t,
+               const hipblasHalf*, hipblasHalf* const*, int64_t, int64_t),
+              (handle, transA, transB, m, n, k, alpha, AP, lda, BP, ldb, beta, CP, ldc, batchCount));
+}
+
+hipblasStatus_t hipblasGemmBatchedEx(hipblasHandle_t handle, hipblasOperation_t transA, hipblasOperation_t transB,
+                                     int m, int n, int k, const void* alpha, const void* A[], hipDataType aType,
+                                     int lda, const void* B[], hipDataType bType, int ldb, const void* beta,
+                                     void* C[], hipDataType cType, int ldc, int batchCount,
+                                     hipblasComputeType_t computeType, hipblasGemmAlgo_t algo) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    vkblas_dtype_t ab, ct;
+    int sf16;
+    if (ex_types((int)aType, (int)bType, (int)cType, (int)computeType, &ab, &ct, &sf16)) {
+        hipblasStatus_t s = run_gemm_batched(handle, ab, ct, sf16, transA, transB, m, n, k, alpha, A, lda, B, ldb,
+                                             beta, C, ldc, batchCount);
+        if (s != VKB_DECLINE) return s;
+    }
+    REAL_CALL(hipblasStatus_t, hipblasGemmBatchedEx,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int, int, int, const void*, const void**,
+               hipDataType, int, const void**, hipDataType, int, const void*, void**, hipDataType, int, int,
+               hipblasComputeType_t, hipblasGemmAlgo_t),
+              (handle, transA, transB, m, n, k, alpha, A, aType, lda, B, bType, ldb, beta, C, cType, ldc, batchCount,
+               computeType, algo));
+}
+
+hipblasStatus_t hipblasGemmBatchedEx_64(hipblasHandle_t handle, hipblasOperation_t transA,
+                                        hipblasOperation_t transB, int64_t m, int64_t n, int64_t k,
+                                        const void* alpha, const void* A[], hipDataType aType, int64_t lda,
+                                        const void* B[], hipDataType bType, int64_t ldb, const void* beta,
+                                        void* C[], hipDataType cType, int64_t ldc, int64_t batchCount,
+                                        hipblasComputeType_t computeType, hipblasGemmAlgo_t algo) {
+    if (!handle) return HIPBLAS_STATUS_INVALID_VALUE;
+    vkblas_dtype_t ab, ct;
+    int sf16;
+    if (ex_types((int)aType, (int)bType, (int)cType, (int)computeType, &ab, &ct, &sf16)) {
+        hipblasStatus_t s = run_gemm_batched(handle, ab, ct, sf16, transA, transB, m, n, k, alpha, A, lda, B, ldb,
+                                             beta, C, ldc, batchCount);
+        if (s != VKB_DECLINE) return s;
+    }
+    REAL_CALL(hipblasStatus_t, hipblasGemmBatchedEx_64,
+              (hipblasHandle_t, hipblasOperation_t, hipblasOperation_t, int64_t, int64_t, int64_t, const void*,
+               const void**, hipDataType, int64_t, const void**, hipDataType, int64_t, const void*, void**,
+               hipDataType, int64_t, int64_t, hipblasComputeType_t, hipblasGemmAlgo_t),
+              (handle, transA, transB, m, n, k, alpha, A, aType, lda, B, bType, ldb, beta, C, cType, ldc, batchCount,
+               computeType, algo));
 }
 
 /* ------------------------------------------------ forward-only GEMMs */

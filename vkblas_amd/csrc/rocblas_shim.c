@@ -117,6 +117,7 @@ typedef struct {
     int64_t batch;
     rocblas_datatype compute_type;
     uint32_t flags;
+    int ptr_array;   /* a, b, c, d: device arrays of batch matrix pointers */
 } gemm_call;
 
 static int op_t(rocblas_operation op) {
@@ -189,8 +190,10 @@ static int run(const gemm_call* g) {
                 (long long)g->m, (long long)g->n, (long long)g->k,
                 (long long)g->lda, (long long)g->ldb, (long long)g->ldc, (long long)g->ldd, (long long)g->batch);
 
-    /* D separate from C: bring C into D first when the epilogue may read it */
-    if (g->c != g->d && beta_maybe_nonzero) {
+    /* D separate from C: bring C into D first when the epilogue may read it
+     * (with pointer arrays the matrices are not known on the host: declined) */
+    if (g->ptr_array && g->c != g->d) return 1;
+    if (!g->ptr_array && g->c != g->d && beta_maybe_nonzero) {
         if (!g->c) return 1;
         const size_t es = ct == VKBLAS_DT_F32 ? 4 : 2;
         for (int64_t i = 0; i < g->batch; ++i) {
@@ -200,11 +203,19 @@ static int run(const gemm_call* g) {
                 return 1;
         }
     }
-    vkblas_status_t st = vkblas_gemm_async(
-        ab, ct, op_t(g->transB) ? VKBLAS_OP_T : VKBLAS_OP_N, op_t(g->transA) ? VKBLAS_OP_T : VKBLAS_OP_N,
-        (uint32_t)g->n, (uint32_t)g->m, (uint32_t)g->k, alpha, g->b, (uint32_t)g->ldb, g->a, (uint32_t)g->lda, beta,
-        g->d, (uint32_t)g->ldd, (uint32_t)g->batch, g->batch > 1 ? g->sb : 0, g->batch > 1 ? g->sa : 0,
-        g->batch > 1 ? g->sd : 0, sm, ad, bd, 0, stream);
+    const vkblas_op_t op_a = op_t(g->transB) ? VKBLAS_OP_T : VKBLAS_OP_N;
+    const vkblas_op_t op_b = op_t(g->transA) ? VKBLAS_OP_T : VKBLAS_OP_N;
+    vkblas_status_t st;
+    if (g->ptr_array)
+        st = vkblas_gemm_batched_async(ab, ct, op_a, op_b, (uint32_t)g->n, (uint32_t)g->m, (uint32_t)g->k, alpha,
+                                       (const void* const*)g->b, (uint32_t)g->ldb, (const void* const*)g->a,
+                                       (uint32_t)g->lda, beta, (void* const*)g->d, (uint32_t)g->ldd,
+                                       (uint32_t)g->batch, sm, ad, bd, stream);
+    else
+        st = vkblas_gemm_async(ab, ct, op_a, op_b, (uint32_t)g->n, (uint32_t)g->m, (uint32_t)g->k, alpha, g->b,
+                               (uint32_t)g->ldb, g->a, (uint32_t)g->lda, beta, g->d, (uint32_t)g->ldd,
+                               (uint32_t)g->batch, g->batch > 1 ? g->sb : 0, g->batch > 1 ? g->sa : 0,
+                               g->batch > 1 ? g->sd : 0, sm, ad, bd, 0, stream);
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return 1;
@@ -245,7 +256,7 @@ rocblas_status(rocblas_gemm_ex)(rocblas_handle handle, rocblas_operation transA,
                                 rocblas_datatype compute_type, rocblas_gemm_algo algo, int32_t solution_index,
                                 uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
-                         c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags};
+                         c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags, 0};
     if (run(&g) == 0) return rocblas_status_success;
     static void* fn;
     gemm_ex_t f = (gemm_ex_t)cached_sym(&fn, "rocblas_gemm_ex");
@@ -262,7 +273,7 @@ rocblas_status(rocblas_gemm_ex_64)(rocblas_handle handle, rocblas_operation tran
                                    rocblas_datatype compute_type, rocblas_gemm_algo algo, int32_t solution_index,
                                    uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
-                         c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags};
+                         c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags, 0};
     if (run(&g) == 0) return rocblas_status_success;
     static void* fn;
     gemm_ex64_t f = (gemm_ex64_t)cached_sym(&fn, "rocblas_gemm_ex_64");
@@ -280,7 +291,7 @@ rocblas_status(rocblas_gemm_strided_batched_ex)(
     rocblas_datatype compute_type, rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, stride_a, b, b_type, ldb,
                          stride_b, beta, c, c_type, ldc, stride_c, d, d_type, ldd, stride_d, batch_count,
-                         compute_type, flags};
+                         compute_type, flags, 0};
     if (run(&g) == 0) return rocblas_status_success;
     static void* fn;
     gemm_sb_t f = (gemm_sb_t)cached_sym(&fn, "rocblas_gemm_strided_batched_ex");
@@ -299,7 +310,7 @@ rocblas_status(rocblas_gemm_strided_batched_ex_64)(
     rocblas_datatype compute_type, rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, stride_a, b, b_type, ldb,
                          stride_b, beta, c, c_type, ldc, stride_c, d, d_type, ldd, stride_d, batch_count,
-                         compute_type, flags};
+                         compute_type, flags, 0};
     if (run(&g) == 0) return rocblas_status_success;
     static void* fn;
     gemm_sb64_t f = (gemm_sb64_t)cached_sym(&fn, "rocblas_gemm_strided_batched_ex_64");
@@ -307,4 +318,53 @@ rocblas_status(rocblas_gemm_strided_batched_ex_64)(
     return f(handle, transA, transB, m, n, k, alpha, a, a_type, lda, stride_a, b, b_type, ldb, stride_b, beta, c,
              c_type, ldc, stride_c, d, d_type, ldd, stride_d, batch_count, compute_type, algo, solution_index,
              flags);
+}
+
+/* Pointer-array batched: no counterpart in the reference (it forwarded
+ * rocblas_gemm_batched_ex).  a, b, c, d are device arrays of batch_count
+ * matrix pointers; a separate D is declined. */
+typedef rocblas_status (*gemm_b_t)(rocblas_handle, rocblas_operation, rocblas_operation, rocblas_int, rocblas_int,
+                                   rocblas_int, const void*, const void*, rocblas_datatype, rocblas_int, const void*,
+                                   rocblas_datatype, rocblas_int, const void*, const void*, rocblas_datatype,
+                                   rocblas_int, void*, rocblas_datatype, rocblas_int, rocblas_int, rocblas_datatype,
+                                   rocblas_gemm_algo, int32_t, uint32_t);
+typedef rocblas_status (*gemm_b64_t)(rocblas_handle, rocblas_operation, rocblas_operation, int64_t, int64_t,
+                                     int64_t, const void*, const void*, rocblas_datatype, int64_t, const void*,
+                                     rocblas_datatype, int64_t, const void*, const void*, rocblas_datatype, int64_t,
+                                     void*, rocblas_datatype, int64_t, int64_t, rocblas_datatype, rocblas_gemm_algo,
+                                     int32_t, uint32_t);
+
+rocblas_status(rocblas_gemm_batched_ex)(rocblas_handle handle, rocblas_operation transA, rocblas_operation transB,
+                                        rocblas_int m, rocblas_int n, rocblas_int k, const void* alpha,
+                                        const void* a, rocblas_datatype a_type, rocblas_int lda, const void* b,
+                                        rocblas_datatype b_type, rocblas_int ldb, const void* beta, const void* c,
+                                        rocblas_datatype c_type, rocblas_int ldc, void* d, rocblas_datatype d_type,
+                                        rocblas_int ldd, rocblas_int batch_count, rocblas_datatype compute_type,
+                                        rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags) {
+    const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
+                         c, c_type, ldc, 0, d, d_type, ldd, 0, batch_count, compute_type, flags, 1};
+    if (run(&g) == 0) return rocblas_status_success;
+    static void* fn;
+    gemm_b_t f = (gemm_b_t)cached_sym(&fn, "rocblas_gemm_batched_ex");
+    if (!f) return rocblas_status_not_implemented;
+    return f(handle, transA, transB, m, n, k, alpha, a, a_type, lda, b, b_type, ldb, beta, c, c_type, ldc, d,
+             d_type, ldd, batch_count, compute_type, algo, solution_index, flags);
+}
+
+rocblas_status(rocblas_gemm_batched_ex_64)(rocblas_handle handle, rocblas_operation transA,
+                                           rocblas_operation transB, int64_t m, int64_t n, int64_t k,
+                                           const void* alpha, const void* a, rocblas_datatype a_type, int64_t lda,
+                                           const void* b, rocblas_datatype b_type, int64_t ldb, const void* beta,
+                                           const void* c, rocblas_datatype c_type, int64_t ldc, void* d,
+                                           rocblas_datatype d_type, int64_t ldd, int64_t batch_count,
+                                           rocblas_datatype compute_type, rocblas_gemm_algo algo,
+                                           int32_t solution_index, uint32_t flags) {
+    const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
+                         c, c_type, ldc, 0, d, d_type, ldd, 0, batch_count, compute_type, flags, 1};
+    if (run(&g) == 0) return rocblas_status_success;
+    static void* fn;
+    gemm_b64_t f = (gemm_b64_t)cached_sym(&fn, "rocblas_gemm_batched_ex_64");
+    if (!f) return rocblas_status_not_implemented;
+    return f(handle, transA, transB, m, n, k, alpha, a, a_type, lda, b, b_type, ldb, beta, c, c_type, ldc, d,
+             d_type, ldd, batch_count, compute_type, algo, solution_index, flags);
 }

@@ -54,6 +54,9 @@ typedef struct vkb_gemm_args {
     const void* beta_dev;
     /* 0: best kernel for the shape; 1: always the generic blocked kernel */
     int generic_only;
+    /* 1: A, B, C are device arrays of `batch` matrix pointers (stride_* are
+     * unused); runs the checked generic kernel, split must be 1 */
+    int ptr_array;
 } vkb_gemm_args;
 
 /* Tile-config properties the dispatcher plans with. */

@@ -42,6 +42,13 @@ _SIGS = {
                                     _i, _ll, _i, _i, _i],
     "hipblasGemmStridedBatchedEx_v2": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _ll, _vp, _i, _i, _ll, _vp, _vp,
                                        _i, _i, _ll, _i, _i, _i],
+    # pointer-array batched: A, B, C are device arrays of matrix pointers
+    # (handle, tA, tB, m, n, k, alpha, A[], lda, B[], ldb, beta, C[], ldc, batch)
+    "hipblasSgemmBatched": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i],
+    "hipblasHgemmBatched": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i],
+    # (handle, tA, tB, m, n, k, alpha, A[], aType, lda, B[], bType, ldb, beta, C[], cType, ldc, batch, compute,
+    #  algo)
+    "hipblasGemmBatchedEx": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _vp, _i, _i, _i, _i, _i],
 }
 
 
