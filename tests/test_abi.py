@@ -147,7 +147,14 @@ def test_plan_forced_split(K, split, dt):
 
 def test_plan_split_heuristic_and_off():
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256)
-    assert pl.path == vk.PATH_SPLITK and 2 <= pl.split <= 64
+    assert pl.path == vk.PATH_SPLITK and 2 <= pl.split <= 256
+    # whole 256x256 tiles: pass 1 on the pipelined kernel, slices of whole K-step pairs
+    assert pl.tile == 2 and pl.k_per_split % 64 == 0
+    pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 262144, 262144, 256, 256)
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 2 and pl.k_per_split % 128 == 0
+    # ragged M: the 128x128 generic split
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 256, 65536, 65536, 256, 256)
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 1
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=1)
     assert pl.path != vk.PATH_SPLITK
     # batched calls never split

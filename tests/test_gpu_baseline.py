@@ -225,6 +225,76 @@ def test_splitk(K, dtype, split):
     assert normwise(to_host(dC1), outs[0]) <= bound
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("mode", ["auto", "ragged"])
+def test_splitk_pipelined(dtype, op_a, op_b, mode):
+    """Split-K pass 1 on the pipelined 256x256 kernel, every layout.
+    auto: the planner's choice at M = N = 256, K = 16384 (a slice per CU,
+    alpha = 1, beta = 0, 16-bit output for 16-bit inputs); ragged: tile forced
+    to 256, a 256 x 512 output, split 7 over K = 8448 (the last slice
+    shorter), alpha / beta on an fp32 C.  Bitwise reproducible run to run."""
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, f32_bound, F16_BOUND, BF16_BOUND
+    auto = mode == "auto"
+    M, N, K = (256, 256, 16384) if auto else (256, 512, 8448)
+    alpha, beta = (1.0, 0.0) if auto else (0.75, -0.5)
+    print(f"[case] splitk pipelined {dtype} op={op_a}{op_b} {mode}", flush=True)
+    lda = M if op_a else K
+    ldb = K if op_b else N
+    a = rng_uniform(300 + op_a, M * K)
+    b = rng_uniform(302 + op_b, K * N)
+    c = rng_uniform(304, M * N)
+    dt = {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}[dtype]
+    conv = {"f32": lambda x: x, "f16": oracle.f2h_rne, "bf16": oracle.f2bf_rne}[dtype]
+    hA, hB = conv(a), conv(b)
+    out16 = auto and dtype != "f32"
+    ct = dt if out16 else vk.DT_F32
+    hC = conv(c) if out16 else c
+    if not auto:
+        vk.set_override(2, False)
+    try:
+        pl = vk.plan(dt, ct, op_a, op_b, M, N, K, lda, ldb, N, split_k=0 if auto else 7)
+        assert pl.path == vk.PATH_SPLITK and pl.tile == 2
+        step2 = 64 if dtype == "f32" else 128
+        assert pl.k_per_split % step2 == 0 and (K - (pl.split - 1) * pl.k_per_split) % step2 == 0
+        if auto:
+            assert pl.split * (M // 256) * (N // 256) >= 64
+        else:
+            assert K - (pl.split - 1) * pl.k_per_split < pl.k_per_split
+        dA, dB = to_dev(hA), to_dev(hB)
+        outs = []
+        for _ in range(2):
+            dC = to_dev(hC)
+            vk.gemm_async(dt, ct, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb, beta,
+                          dC.data_ptr(), N, split_k=0 if auto else 7)
+            assert vk.last_path() == vk.PATH_SPLITK
+            outs.append(to_host(dC))
+    finally:
+        vk.set_override(-1, False)
+    assert np.array_equal(outs[0], outs[1])
+    rows = oracle.sample_rows(M, 12)
+    sel = (rows[:, None] * N + np.arange(N)[None, :]).reshape(-1)
+    ref = hC.copy()
+    if dtype == "f32":
+        oracle.ref_gemm_f32_rm(op_a, op_b, M, N, K, hA, lda, hB, ldb, alpha, beta, ref, N, rows=rows)
+        assert normwise(outs[0][sel], ref[sel]) <= f32_bound(K)
+    elif dtype == "f16":
+        if out16:
+            oracle.ref_gemm_f16_rm(op_a, op_b, M, N, K, hA, lda, hB, ldb, alpha, beta, ref, N, rows=rows)
+            assert normwise(oracle.h2f(outs[0][sel]), oracle.h2f(ref[sel])) <= F16_BOUND
+        else:
+            oracle.ref_gemm_f16f32_rm(op_a, op_b, M, N, K, hA, lda, hB, ldb, alpha, beta, ref, N, rows=rows)
+            assert normwise(outs[0][sel], ref[sel]) <= F16_BOUND
+    else:
+        if out16:
+            oracle.ref_gemm_bf16_rm(op_a, op_b, M, N, K, hA, lda, hB, ldb, alpha, beta, ref, N, rows=rows)
+            assert normwise(oracle.bf2f(outs[0][sel]), oracle.bf2f(ref[sel])) <= BF16_BOUND
+        else:
+            oracle.ref_gemm_bf16f32_rm(op_a, op_b, M, N, K, hA, lda, hB, ldb, alpha, beta, ref, N, rows=rows)
+            assert normwise(outs[0][sel], ref[sel]) <= F16_BOUND
+
+
 @pytest.mark.parametrize("trans", ["NN", "TT"])
 def test_splitk_fp16_out_alpha_beta(trans):
     """split-K pass 2 applies alpha/beta once and rounds once to fp16."""

@@ -1,7 +1,8 @@
 // gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp16 and fp32.
 //
 // Used for full tiles (M, N multiples of 256, K a multiple of two K steps,
-// aligned operands); edges and small shapes use gemm_kernel<> in
+// aligned operands), also as split-K pass 1 (one K slice per workgroup row
+// of the grid, raw fp32 sums); edges and small shapes use gemm_kernel<> in
 // gemm_mfma.hpp, whose MFMA role swap and epilogue this kernel shares.
 // Replaces the reference's large tiles (gemm_f32_128x128_bankfree_tmpl.comp,
 // gemm_half_128x256_bankfree_tmpl.comp, gemm_half_128x128_bankfree_tmpl.comp,
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     const uint32_t nwg = gridDim.x;
     if ((nwg & 7u) == 0) bid = (bid & 7u) * (nwg >> 3) + (bid >> 3);
     const uint32_t per = p.tiles_m * p.tiles_n;
-    const uint32_t b = bid / per;
+    const uint32_t b = bid / per;                   // batch, or K slice under split-K
     const uint32_t t = bid - b * per;
     constexpr uint32_t GM = 8;
     const uint32_t width = GM * p.tiles_n;
@@ -96,14 +97,21 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     const int n0 = (int)(tin / gm) * BN;
 
     const int lda = (int)p.lda, ldb = (int)p.ldb;
+    // Split-K pass 1 (split > 1, batch 1): slice b covers k in
+    // [b kps, min(K, (b + 1) kps)) and writes raw sums to C + b s_split.  The
+    // launcher makes kps and K multiples of two K steps, so every slice is.
+    const bool sk = p.split > 1;
+    const int64_t kbeg = sk ? (int64_t)b * p.kps : 0;
+    const uint32_t klen = sk ? min(p.K - (uint32_t)kbeg, p.kps) : p.K;
+    const int64_t bat = sk ? 0 : (int64_t)b;
     // Buffer resources on the tile's first element; all per-lane parts are
     // 32-bit byte offsets (the launcher guarantees they fit).
-    const T* At = (const T*)p.A + (int64_t)b * p.sa + (AK ? (int64_t)m0 * p.lda : (int64_t)m0);
-    const T* Bt = (const T*)p.B + (int64_t)b * p.sb + (BKM ? (int64_t)n0 * p.ldb : (int64_t)n0);
+    const T* At = (const T*)p.A + bat * p.sa + (AK ? (int64_t)m0 * p.lda + kbeg : kbeg * p.lda + m0);
+    const T* Bt = (const T*)p.B + bat * p.sb + (BKM ? (int64_t)n0 * p.ldb + kbeg : kbeg * p.ldb + n0);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)At, (short)0, -1, 0x00020000);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc((void*)Bt, (short)0, -1, 0x00020000);
-    TC* Cb = (TC*)p.C + (int64_t)b * p.sc;
-    const int nkt = (int)(p.K / BK);
+    TC* Cb = (TC*)p.C + (sk ? (int64_t)b * p.s_split : (int64_t)b * p.sc);
+    const int nkt = (int)(klen / BK);
 
     // K-major direct loads: instruction i of this wave fills the 8-row group
     // 8 wave + i (rows 64 wave + 8 i + [0, 8); lane -> row + lane / 8, slot
