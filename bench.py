@@ -63,6 +63,24 @@ class Timer:
         return [s.elapsed_time(e) for s, e in self.pairs]
 
 
+def batch_ms(torch, stream, fn, launches, batches=5):
+    """Median over `batches` of the average launch duration of `launches`
+    back-to-back calls fn(i) between one pair of HIP events on `stream` (a
+    per-launch event pair adds its own gap to a launch of a few tens of us)."""
+    avgs, i = [], 0
+    for _ in range(batches):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(launches):
+            fn(i)
+            i += 1
+        e.record(stream)
+        torch.cuda.synchronize()
+        avgs.append(s.elapsed_time(e) / launches)
+    avgs.sort()
+    return avgs[len(avgs) // 2]
+
+
 def fp32_headline(torch, vk, stream, steps, warmup):
     """the four hipBLAS transpose variants at 4096^3."""
     n = 4096
@@ -118,11 +136,7 @@ def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False):
                           C.data_ptr(), n, stream=sp)
         for _ in range(3):
             call()
-        timer = Timer(torch, stream)
-        for _ in range(max(steps, 20)):
-            timer.run(call)
-        ts = sorted(timer.times_ms())
-        med = ts[len(ts) // 2]
+        med = batch_ms(torch, stream, lambda i: call(), max(steps, 20))
         out[name] = {"ms": round(med, 4), "tflops": round(2.0 * n ** 3 / (med * 1e-3) / 1e12, 1),
                      "path": vk.PATH_NAMES[vk.last_path()]}
         out[name]["frac_of_peak"] = round(out[name]["tflops"] / PEAK_FP16_TFLOPS, 4)
@@ -147,11 +161,7 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
                           Ws[i % 3].data_ptr(), K, 0.0, Y.data_ptr(), O, stream=sp)
         for i in range(6):
             call(i)
-        timer = Timer(torch, stream)
-        for i in range(max(steps, 30)):
-            timer.run(lambda i=i: call(i))
-        ts = sorted(timer.times_ms())
-        med = ts[len(ts) // 2]
+        med = batch_ms(torch, stream, call, 3 * max(steps, 10))
         nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
         gbs = nbytes / (med * 1e-3) / 1e9
         out[f"n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(gbs, 1), "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 4),
@@ -315,11 +325,7 @@ def splitk(torch, vk, stream, steps):
                                   stream=sp)
                 for _ in range(3):
                     call()
-                timer = Timer(torch, stream)
-                for _ in range(max(steps, 10)):
-                    timer.run(call)
-                ts = sorted(timer.times_ms())
-                med = ts[len(ts) // 2]
+                med = batch_ms(torch, stream, lambda i: call(), max(steps, 10))
                 tf = 2.0 * 256 * 256 * K / (med * 1e-3) / 1e12
                 gbs = (A.numel() + B.numel()) * A.element_size() / (med * 1e-3) / 1e9
                 key = f"K{K}_{dt}_s{split}" if split else f"K{K}_{dt}_auto"
@@ -345,11 +351,7 @@ def batched(torch, vk, stream, steps):
                       n, nb, n * n, n * n, n * n, stream=sp)
     for _ in range(3):
         call()
-    timer = Timer(torch, stream)
-    for _ in range(max(steps, 20)):
-        timer.run(call)
-    ts = sorted(timer.times_ms())
-    med = ts[len(ts) // 2]
+    med = batch_ms(torch, stream, lambda i: call(), max(steps, 20))
     tf = 2.0 * nb * n ** 3 / (med * 1e-3) / 1e12
     return {"ms": round(med, 4), "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_FP32_TFLOPS, 4),
             "path": vk.PATH_NAMES[vk.last_path()]}
