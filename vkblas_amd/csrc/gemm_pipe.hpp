@@ -1,4 +1,4 @@
-// gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp16 and fp32.
+// gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp32, fp16 and bf16.
 //
 // Used for full tiles (M, N multiples of 256, K a multiple of two K steps,
 // aligned operands), also as split-K pass 1 (one K slice per workgroup row
@@ -9,43 +9,53 @@
 // dispatched from src/vkblas.c:1191-1313, 1822-1868).
 //
 // Per workgroup: 4 waves, 2x2, each owning a 128x128 block of C held in 256
-// AGPRs.  A K step is 128 bytes of K (64 fp16 or 32 fp32):
-//  * fp16, both operands K-major: two sub-steps of v_mfma_f32_16x16x32_f16
-//    on 8x8 16x16 tiles (64 MFMAs each; lane group g = lane / 16 takes chunk
-//    4s + g);
-//  * fp16 with an MN-major operand: four sub-steps of
-//    v_mfma_f32_32x32x16_f16 on 4x4 32x32 tiles (chunk 2s + h, 16 MFMAs);
+// AGPRs.  A K step is 128 bytes of K (64 fp16 / bf16 or 32 fp32):
+//  * 16-bit types, every layout: two sub-steps of v_mfma_f32_16x16x32 on 8x8
+//    16x16 tiles (64 MFMAs each; lane group g = lane / 16 takes k 8g..8g+7 of
+//    the sub-step's 32);
 //  * fp32: four sub-steps of v_mfma_f32_32x32x2_f32 on 4x4 32x32 tiles (one
 //    MFMA per k of chunk 4h + s, 64 MFMAs each).
 // Per K step:
-//  * K-major operand tiles go global -> LDS directly (buffer_load ... lds:
-//    lane l of a wave writes 16 B at M0 + 16 l), so they use no VGPRs and no
-//    ds_write.  Each instruction fills eight whole 128-byte LDS rows; lane l
-//    fetches the global chunk that the swizzle maps to its LDS slot, so the
-//    global side stays fully coalesced.
-//  * An MN-major operand tile goes through VGPRs: VEC x VEC blocks
-//    transposed in registers and written K-contiguous (8 ds_write_b128 per
-//    lane).
+//  * Operand tiles go global -> LDS directly (buffer_load ... lds: lane l of
+//    a wave writes 16 B at M0 + 16 l), so they use no VGPRs and no ds_write;
+//    lane l fetches the global chunk that the LDS swizzle maps to its slot,
+//    so the global side stays fully coalesced.  Exception: an fp32 MN-major
+//    operand goes through VGPRs (VEC x VEC blocks transposed in registers and
+//    written K-contiguous, 8 ds_write_b128 per lane).
+//  * A 16-bit MN-major operand stays MN-major in LDS and its fragments are
+//    read with ds_read_b64_tr_b16: within each 16-lane group, lane i receives
+//    element i & 3 of the 8 bytes addressed by lanes (i >> 2) + 4 j, j = 0..3.
+//    Lane q of group g addressing row k = 8g + (q >> 2) (+4 for the second
+//    read), columns 4 (q & 3) .. +3 of the fragment, therefore receives k
+//    8g .. 8g+3 (then +4 .. +7) of column q: the MFMA operand layout.
 //  * Loads for K step t+1 are issued during step t into the other LDS stage;
 //    MFMA fragments for sub-step s+1 are read from LDS while the MFMAs of
 //    sub-step s run (two register sets).
-//  * One barrier per K step.  The K loop is unrolled by two so both LDS
-//    stages are compile-time offsets.
+//  * One barrier per K step.
 //
 // LDS map (16-byte units): A stage s at s*2304, B stage s at 4608 + s*2304
 // (144 KB).  gfx950's LDS is 64 banks (256 bytes) wide and serves a
 // ds_read_b128 16 lanes at a time, so the 16 rows a fragment read touches at
 // one chunk must land on 16 distinct 16-byte bank groups: the 8 rows of one
 // row parity share a 256-byte bank line half and need 8 distinct slots.
-//  * MN-major tiles (written transposed through VGPRs): row r at r*8, chunk c
-//    at slot c ^ g(r), g(r) = (r ^ (r >> 3)) & 7 — over 16 consecutive rows
-//    each parity class sees all 8 slots.
+//  * fp32 MN-major tiles (written transposed through VGPRs): row r at r*8,
+//    chunk c at slot c ^ g(r), g(r) = (r ^ (r >> 3)) & 7 — over 16
+//    consecutive rows each parity class sees all 8 slots.
 //  * K-major tiles (written by whole-row DMA, lane l -> +16 l, so the swizzle
 //    can only depend on r & 7): rows come in groups of 8 at a 1152-byte
 //    stride (72 units, 128 bytes of padding per group), row r at
 //    (r >> 3)*72 + (r & 7)*8, chunk c at slot c ^ (r & 7).  The padding
 //    moves odd groups to the other half of the bank line, which separates
 //    rows r and r + 8 that share r & 7.
+//  * 16-bit MN-major tiles (k rows of 256 m or n, 32 chunks): rows k, k+1
+//    form a 1-KiB block (one DMA instruction) at (k >> 1)*64, row k & 1 at
+//    +32, chunk c at slot c ^ t(k), t(k) = 2 (k & 3) + 8 (((k >> 3) ^
+//    (k >> 4)) & 1).  A transposing read of 32 lanes touches rows
+//    {8g + 0..3} of two lane groups at two chunks 2i, 2i + 1: t takes 8
+//    distinct even values over those rows for either pairing of the four
+//    groups ((0,1)(2,3) or (0,2)(1,3)), so the 16 chunks fall on 16 distinct
+//    16-byte bank groups.  t(k + 4) = t(k) for the second read and
+//    t(k + 32) = t(k) for the second sub-step, so both are immediate offsets.
 // Every row base has its low three bits clear, so a fragment's slot index is
 // (base + (hoff ^ g)) ^ sub-step offset (4s, 2s or s by MFMA shape).
 //
@@ -59,6 +69,10 @@
 namespace vkb {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
 #ifndef VKB_PIPE_DMA_UNITS
 #define VKB_PIPE_DMA_UNITS 16
@@ -121,6 +135,20 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     const int koff = ((lane & 7) ^ (lane >> 3)) << 4;
     const int a_voff = (64 * wave + (lane >> 3)) * lda * ES + koff;
     const int b_voff = (64 * wave + (lane >> 3)) * ldb * ES + koff;
+    // 16-bit MN-major direct loads: instruction n of this wave fills the
+    // 1-KiB block 8 wave + n (k rows 2 (8 wave + n) + [0, 2); lane -> row +
+    // lane / 32, slot lane % 32, which holds chunk (lane % 32) ^ t(row)).
+    // t(row) depends on n only through n & 1 and n >> 2, so four VGPR offsets
+    // serve the eight instructions; the row step and k0 go in soffset.
+    constexpr bool ATR = F16 && !AK, BTR = F16 && !BKM;
+    auto tsw = [](int k) { return 2 * (k & 3) + 8 * (((k >> 3) ^ (k >> 4)) & 1); };
+    int a_tr[4], b_tr[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int k = 2 * (8 * wave + ((v & 1) | ((v >> 1) << 2))) + h;
+        a_tr[v] = h * lda * ES + (((lane & 31) ^ tsw(k)) << 4);
+        b_tr[v] = h * ldb * ES + (((lane & 31) ^ tsw(k)) << 4);
+    }
     // MN-major staged loads: VECxVEC blocks (kb, mb + 32 blk), kb = tid / 32
     // (k rows kb*VEC..), mb = tid % 32 (columns (mb + 32 blk)*VEC..)
     const int kb = tid >> 5, mb = tid & 31;
@@ -132,33 +160,63 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     // (no __syncthreads) because its workgroup fence would wait for every
     // outstanding load; the "memory" clobber keeps the compiler from moving
     // LDS accesses across it.
-    constexpr int NSTAGED = (AK ? 0 : 8) + (BKM ? 0 : 8);
+    constexpr bool STAGED = !F16 && (!AK || !BKM);  // fp32 MN-major operand through VGPRs
+    constexpr int NSTAGED = STAGED ? (AK ? 0 : 8) + (BKM ? 0 : 8) : 0;
     auto sync_vm = [](auto n_c) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(decltype(n_c)::value) : "memory");
     };
 
     // staged registers: index blk * VEC + k row within the block
-    u32x4 sa_v[AK ? 1 : 8], sb_v[BKM ? 1 : 8];
+    u32x4 sa_v[(STAGED && !AK) ? 8 : 1], sb_v[(STAGED && !BKM) ? 8 : 1];
 
+    // With a transposed-read operand every DMA is issued as inline assembly.
+    // The compiler waits for all LDS DMA in flight (vmcnt) before each
+    // ds_read_b64_tr_b16 it emits, which would serialize the loads behind the
+    // reads; as assembly the DMA is outside its wait-count tracking.  The
+    // end-of-step "s_waitcnt vmcnt(0)" + barrier (sync_vm) is what orders a
+    // step's DMA before any read of its stage, and these kernels have no
+    // other vector-memory load in flight in the K loop.
+    constexpr bool ASM_DMA = ATR || BTR;
+    auto rsrc_words = [](const void* base) {
+        const uint64_t a = (uint64_t)base;
+        return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff), -1, 0x00020000};
+    };
+    const i32x4 ra_w = rsrc_words(At), rb_w = rsrc_words(Bt);
+    auto dma = [&](bool isA, lds_ptr_t dst, int voff, int soff) {
+        if constexpr (ASM_DMA) {
+            const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)dst);
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                         :: "v"(voff), "s"(isA ? ra_w : rb_w), "s"(__builtin_amdgcn_readfirstlane(soff)),
+                            "{m0}"(m0));
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? ra : rb, dst, 16, voff, soff, 0, 0);
+        }
+    };
     // Direct (DMA) load n of K step kt (8 per operand per wave: A then B)
     auto dma_load = [&](int kt, int S, int n) {
         const int k0 = kt * BK;
         if (n < 8) {
             if constexpr (AK)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)&lds[A0 + S * STG + (8 * wave + n) * GRP], 16,
-                                                         a_voff, (k0 + n * 8 * lda) * ES, 0, 0);
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (8 * wave + n) * GRP], a_voff, (k0 + n * 8 * lda) * ES);
+            else if constexpr (ATR)
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (8 * wave + n) * 64], a_tr[(n & 1) | ((n >> 2) << 1)],
+                    (k0 + 2 * (8 * wave + n)) * lda * ES);
         } else {
+            const int m = n - 8;
             if constexpr (BKM)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)&lds[B0 + S * STG + (8 * wave + n - 8) * GRP],
-                                                         16, b_voff, (k0 + (n - 8) * 8 * ldb) * ES, 0, 0);
+                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (8 * wave + m) * GRP], b_voff, (k0 + m * 8 * ldb) * ES);
+            else if constexpr (BTR)
+                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (8 * wave + m) * 64], b_tr[(m & 1) | ((m >> 2) << 1)],
+                    (k0 + 2 * (8 * wave + m)) * ldb * ES);
         }
     };
     // MN-major staged load v of K step kt (8 per operand)
     auto stage_load = [&](int kt, int v) {
         const int k0 = kt * BK + (v % VEC);
         const int blk = v / VEC;
-        if constexpr (!AK) sa_v[v] = __builtin_amdgcn_raw_buffer_load_b128(ra, mn_off(lda, blk), k0 * lda * ES, 0);
-        if constexpr (!BKM) sb_v[v] = __builtin_amdgcn_raw_buffer_load_b128(rb, mn_off(ldb, blk), k0 * ldb * ES, 0);
+        if constexpr (STAGED && !AK) sa_v[v] = __builtin_amdgcn_raw_buffer_load_b128(ra, mn_off(lda, blk), k0 * lda * ES, 0);
+        if constexpr (STAGED && !BKM) sb_v[v] = __builtin_amdgcn_raw_buffer_load_b128(rb, mn_off(ldb, blk), k0 * ldb * ES, 0);
     };
     // MN-major tiles use the swizzle g(r) = (r ^ (r >> 3)) & 7 (swz), which
     // keeps the transposed writes of lanes on distinct banks.  Row v of the
@@ -166,31 +224,26 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     auto stage_store = [&](int S, int v) {
         const int blk = v / VEC, i = v % VEC;
         const int r = (mb + 32 * blk) * VEC + i;
-        if constexpr (!AK) lds[A0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sa_v[blk * VEC], i);
-        if constexpr (!BKM) lds[B0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sb_v[blk * VEC], i);
+        if constexpr (STAGED && !AK) lds[A0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sa_v[blk * VEC], i);
+        if constexpr (STAGED && !BKM) lds[B0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sb_v[blk * VEC], i);
     };
-    constexpr bool STAGED = !AK || !BKM;
 
     // ---- MFMA shape --------------------------------------------------------
-    // SH 0, fp16 with both operands K-major: v_mfma_f32_16x16x32_f16; a
-    //   sub-step is one 32-wide k slice (chunks 4s + g, lane group
-    //   g = lane / 16 holds 8 k of row lane % 16); the wave's 128x128 block is
-    //   8x8 tiles of 16x16 (floatx4).  With random data gfx950 sustains ~15%
-    //   more fp16 FLOP/s on 16x16x32 than on 32x32x16 (half the accumulator
-    //   traffic per FLOP under the power limit).
-    // SH 1, fp16 with a staged (MN-major) operand: v_mfma_f32_32x32x16_f16,
-    //   sub-step s = chunk 2s + h, 4x4 tiles of 32x32 (floatx16); the staged
-    //   registers leave no room for the 16x16 shape's fragment sets.
+    // SH 0, 16-bit types: v_mfma_f32_16x16x32; a sub-step is one 32-wide k
+    //   slice (lane group g = lane / 16 holds 8 k of row lane % 16); the
+    //   wave's 128x128 block is 8x8 tiles of 16x16 (floatx4).  With random
+    //   data gfx950 sustains ~15% more fp16 FLOP/s on 16x16x32 than on
+    //   32x32x16 (half the accumulator traffic per FLOP under the power limit).
     // SH 2, fp32: v_mfma_f32_32x32x2_f32, sub-step s = chunk 4h + s (one MFMA
     //   per k), 4x4 tiles of 32x32.
-    constexpr int SH = F16 ? ((AK && BKM) ? 0 : 1) : 2;
+    constexpr int SH = F16 ? 0 : 2;
     constexpr int NSUB = SH == 0 ? 2 : 4;           // sub-steps per K step
     constexpr int UPS = 32 / NSUB;                  // units per sub-step
     constexpr int NF = SH == 0 ? 8 : 4;             // fragments per operand
     constexpr int FR = SH == 0 ? 16 : 32;           // rows per fragment
-    constexpr int SX = SH == 0 ? 4 : (SH == 1 ? 2 : 1);   // sub-step slot offset
+    constexpr int SX = SH == 0 ? 4 : 1;             // sub-step slot offset
     const int fl = SH == 0 ? (lane & 15) : l32;     // fragment row of this lane
-    const int hoff = SH == 0 ? (lane >> 4) : (SH == 1 ? h : 4 * h);   // chunk in sub-step 0
+    const int hoff = SH == 0 ? (lane >> 4) : 4 * h; // chunk in sub-step 0
 
     // Fragment slot of row r: row base + (hoff ^ g(r)); sub-step s reads it
     // ^ (s * SX).  Fragment i starts FR rows further on (FR = 16 or 32, a
@@ -217,6 +270,24 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
             xb[c] = B0 + b0 + (bg ^ c);
         }
     }
+    // Transposed-read fragments (16-bit MN-major tiles): lane q of group g
+    // reads row k = 8g + (q >> 2) at columns 16 i + 4 (q & 3) .. +3 of the
+    // wave's 128; its unit is (k >> 1) 64 + (k & 1) 32 + (c ^ t(k)) with
+    // c = 16 w + 2 i + ((q >> 1) & 1) and t(k) = 2 (q >> 2) + 8 ((g ^ g >> 1)
+    // & 1) (even, below 16), plus 8 bytes for odd q.  Per fragment i that is
+    // a per-lane base with (2 i ^ t); the second read (+4 rows: +2048 bytes),
+    // the second sub-step (+32 rows: +16384 bytes) and the stage are offsets.
+    int tra[8], trb[8];   // bytes
+    {
+        const int g = lane >> 4, q = lane & 15;
+        const int tk = 2 * (q >> 2) + 8 * ((g ^ (g >> 1)) & 1);
+        const int L = (4 * g + (q >> 3)) * 64 + ((q >> 2) & 1) * 32 + ((q >> 1) & 1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            tra[i] = (A0 + L + 16 * wm + ((2 * i) ^ tk)) * 16 + (q & 1) * 8;
+            trb[i] = (B0 + L + 16 * wn + ((2 * i) ^ tk)) * 16 + (q & 1) * 8;
+        }
+    }
 
     using acc_t = std::conditional_t<SH == 0, floatx4, floatx16>;
     constexpr int AR = SH == 0 ? 4 : 16;            // accumulator registers per tile
@@ -228,36 +299,53 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 #pragma unroll
             for (int r = 0; r < AR; ++r) acc[i][j][r] = 0.0f;
 
-    // A sub-step is UPS units; each unit also reads one fragment of the next
+    // A sub-step is UPS units; its units also read the fragments of the next
     // sub-step, in the order the next sub-step first uses them.
-    // SH 0: unit q = tiles (q/2, 4(q%2) .. +3): reads B0-B3 A0 B4-B7 A1 .. A7.
-    //   A_i is last used by unit 2i+1 and its successor is read in a later
-    //   unit (A0 at 4, A_i at 8+i), so A needs one register set; B needs two.
-    // SH 1: unit q = tiles (q/2, 2(q%2) .. +1): reads B0 B1 A0 B2 B3 A1 A2 A3.
+    // SH 0: unit q = tiles (q/2, 4(q%2) .. +3): reads B0-B3 A0 B4-B7 A1 .. A7,
+    //   a transposed-read fragment as two reads; the NRD reads are dealt over
+    //   the 16 units in order.  With K-major A, A_i is last used by unit 2i+1
+    //   and its successor is read in that unit or a later one, so A needs one
+    //   register set; a transposed-read A (two reads each) comes earlier and
+    //   takes two, as B always does.
     // SH 2: unit q = k element q/2 of the chunk on tiles (2(q%2) .. +1, 0..3):
-    //   reads B0..B3 A0..A3.
-    // SH 1 and 2 keep every fragment to the sub-step's end: two sets each.
-    constexpr int NAB = SH == 0 ? 1 : 2;
+    //   reads B0..B3 A0..A3, every fragment kept to the sub-step's end: two
+    //   sets each.
+    constexpr int NAB = (SH == 0 && !ATR) ? 1 : 2;
+    constexpr int NRD = 16 + (ATR ? 8 : 0) + (BTR ? 8 : 0);   // SH 0 reads per sub-step
     u32x4 af[NAB][NF], bf[2][NF];
-    auto read_one = [&](int buf, int S, int s, int idx) {
-        bool isA;
-        int fi;
+    auto tr_half = [&](u32x4& dst, int half, int byte_off) {
+        const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((char*)lds + byte_off));
+        const u32x2 w = __builtin_bit_cast(u32x2, v);
+        dst[2 * half] = w[0];
+        dst[2 * half + 1] = w[1];
+    };
+    auto frag_read = [&](int buf, int S, int s, bool isA, int fi, int half) {
+        if (isA) {
+            if constexpr (ATR) tr_half(af[buf % NAB][fi], half, tra[fi] + S * STG * 16 + s * 16384 + half * 2048);
+            else af[buf % NAB][fi] = lds[xa[dsw(AK, fi) ^ (SX * s)] + S * STG + fi * ASTEP];
+        } else {
+            if constexpr (BTR) tr_half(bf[buf][fi], half, trb[fi] + S * STG * 16 + s * 16384 + half * 2048);
+            else bf[buf][fi] = lds[xb[dsw(BKM, fi) ^ (SX * s)] + S * STG + fi * BSTEP];
+        }
+    };
+    auto read_one = [&](int buf, int S, int s, int q) {   // the reads of unit q
         if constexpr (SH == 0) {
             constexpr int isA16[16] = {0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1};
             constexpr int fi16[16] = {0, 1, 2, 3, 0, 4, 5, 6, 7, 1, 2, 3, 4, 5, 6, 7};
-            isA = isA16[idx];
-            fi = fi16[idx];
-        } else if constexpr (SH == 1) {
-            constexpr int isA8[8] = {0, 0, 1, 0, 0, 1, 1, 1};
-            constexpr int fi8[8] = {0, 1, 0, 2, 3, 1, 2, 3};
-            isA = isA8[idx];
-            fi = fi8[idx];
+            int o = 0;   // read index in the sub-step's sequence
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const bool tr = isA16[t] ? ATR : BTR;
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    if (half == 1 && !tr) continue;
+                    if (o * 16 >= q * NRD && o * 16 < (q + 1) * NRD) frag_read(buf, S, s, isA16[t], fi16[t], half);
+                    ++o;
+                }
+            }
         } else {
-            isA = idx >= 4;
-            fi = idx & 3;
+            frag_read(buf, S, s, q >= 4, q & 3, 0);
         }
-        if (isA) af[buf % NAB][fi] = lds[xa[dsw(AK, fi) ^ (SX * s)] + S * STG + fi * ASTEP];
-        else bf[buf][fi] = lds[xb[dsw(BKM, fi) ^ (SX * s)] + S * STG + fi * BSTEP];
     };
     auto mfma_unit = [&](int buf, int q) {
         if constexpr (SH == 0) {
@@ -265,11 +353,6 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 #pragma unroll
             for (int j = j0; j < j0 + 4; ++j)
                 acc[i][j] = mfma_16x16x32<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
-        } else if constexpr (SH == 1) {
-            const int i = q >> 1, j0 = (q & 1) * 2;
-#pragma unroll
-            for (int j = j0; j < j0 + 2; ++j)
-                acc[i][j] = mfma_32x32x16<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
         } else {
             const int e = q >> 1, i0 = (q & 1) * 2;
 #pragma unroll
@@ -359,9 +442,9 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
             // (stages 1 and 0 as constants) the register allocator gives the
             // accumulator tiles different registers in the two halves and
             // copies them around on every iteration (AGPR moves and parking
-            // in VGPRs, ~100 extra VALU per two K steps).  The other shapes
-            // keep the constant stages: their staged stores' addresses fold
-            // into immediates, and they show no such copies.
+            // in VGPRs, ~100 extra VALU per two K steps).  The fp32 shape
+            // keeps the constant stages: its staged stores' addresses fold
+            // into immediates, and it shows no such copies.
 #pragma clang loop unroll(disable)
             for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, true);
             region(kt, kt & 1, true, true, false);             // kt == nkt - 2: loads step nkt-1
