@@ -42,11 +42,13 @@
 //    chunk c at slot c ^ g(r), g(r) = (r ^ (r >> 3)) & 7 — over 16
 //    consecutive rows each parity class sees all 8 slots.
 //  * K-major tiles (written by whole-row DMA, lane l -> +16 l, so the swizzle
-//    can only depend on r & 7): rows come in groups of 8 at a 1152-byte
-//    stride (72 units, 128 bytes of padding per group), row r at
-//    (r >> 3)*72 + (r & 7)*8, chunk c at slot c ^ (r & 7).  The padding
-//    moves odd groups to the other half of the bank line, which separates
-//    rows r and r + 8 that share r & 7.
+//    can only depend on r & 7): chunk c of row r at slot c ^ (r & 7), rows
+//    in groups of 8 at (r >> 3)*GRP + (r & 7)*8.  16-bit types read 16-row
+//    fragments and use GRP = 64 (no padding): measured free of bank
+//    conflicts, while a 128-byte pad per group gives them 1.5x the LDS read
+//    time.  fp32 reads 32-row fragments and uses GRP = 72 (1152-byte group
+//    stride): the pad moves odd groups to the other half of the bank line,
+//    which separates rows r and r + 8 that share r & 7.
 //  * 16-bit MN-major tiles (k rows of 256 m or n, 32 chunks): rows k, k+1
 //    form a 1-KiB block (one DMA instruction) at (k >> 1)*64, row k & 1 at
 //    +32, chunk c at slot c ^ t(k), t(k) = 2 (k & 3) + 8 (((k >> 3) ^
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     constexpr int BM = 256, BN = 256, BK = 128 / ES;
     constexpr int VEC = 16 / ES;                    // elements per 16-byte chunk
     constexpr int A0 = 0, B0 = 4608, STG = 2304;    // u32x4 offsets
-    constexpr int GRP = 72;                         // 8-row group stride of K-major tiles
+    constexpr int GRP = F16 ? 64 : 72;              // 8-row group stride of K-major tiles
     __shared__ u32x4 lds[9216];                     // 144 KB
 
     const int tid = threadIdx.x;
