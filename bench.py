@@ -32,8 +32,8 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 # HBM bytes per launch of the fp32 4096^3 256x256 GEMM kernel: rocprofv3
 # FETCH_SIZE and WRITE_SIZE passes over this benchmark (KiB per dispatch,
 # averaged over the four variants), scaled by what the same counters read
-# for a 256 MiB device copy (FETCH x2.00, WRITE x1.00).  Summaries:
-# profiles/gemm_skinny_bench_traffic.txt, profiles/copy_256MiB_traffic_calibration.txt.
+# for a 256 MiB device copy (FETCH x2.00, WRITE x1.00).  Summary:
+# profiles/hbm_traffic_bench_legs.txt.
 TRAFFIC_F32_4096_BYTES = int((2.00 * 198440.0 + 1.00 * 68736.0) * 1024)
 
 METRIC = "TFLOPS 4096³ fp32/fp16 GEMM (% MFMA peak); fp16 matvec GB/s (% HBM peak)"
@@ -222,7 +222,7 @@ def main():
     stream = torch.cuda.current_stream()
 
     if args.only == "fp16":
-        print(json.dumps(fp16_gemm(torch, vk, stream, args.steps)))
+        print(json.dumps({n: fp16_gemm(torch, vk, stream, args.steps, n=n) for n in (2048, 4096, 8192)}))
         return
     if args.only == "bf16":
         print(json.dumps(fp16_gemm(torch, vk, stream, args.steps, bf16=True)))
@@ -287,6 +287,15 @@ def main():
     line["bf16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps, bf16=True)
     log("[bench] bf16 matvec 8192x8192")
     line["bf16_matvec_8192"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8), bf16=True)
+    log("[bench] fp16 2048^3 and 8192^3")
+    line["fp16_gemm_2048"] = fp16_gemm(torch, vk, stream, args.steps, n=2048)
+    line["fp16_gemm_8192"] = fp16_gemm(torch, vk, stream, args.steps, n=8192)
+    log("[bench] decode 4096x14336 / 14336x4096")
+    line["fp16_matvec_4096x14336"] = matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 16))
+    line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 16))
+    log("[bench] split-K and strided-batched")
+    line["splitk_256x256"] = splitk(torch, vk, stream, args.steps, splits=(0,))
+    line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
     print(json.dumps(line), flush=True)
 
 
@@ -307,8 +316,8 @@ def calibrate(torch, stream, mib=256, reps=5):
     return {"copy_bytes_read": n, "copy_bytes_written": n, "ms": sorted(ts)[len(ts) // 2]}
 
 
-def splitk(torch, vk, stream, steps):
-    """M=N=256 tall-K split-K, fp32 and fp16, split {4,16,64} and the planner's choice."""
+def splitk(torch, vk, stream, steps, splits=(4, 16, 64, 0)):
+    """M=N=256 tall-K split-K, fp32 and fp16, split {4,16,64} and the planner's choice (0)."""
     sp = stream.cuda_stream
     out = {}
     for K in (65536, 262144):
@@ -318,7 +327,7 @@ def splitk(torch, vk, stream, steps):
             if dt == "f16":
                 A, B = A.half(), B.half()
             C = torch.empty(256 * 256, device="cuda:0")
-            for split in (4, 16, 64, 0):   # 0: the planner's choice
+            for split in splits:
                 def call():
                     vk.gemm_async(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, 1.0,
                                   A.data_ptr(), K, B.data_ptr(), 256, 0.0, C.data_ptr(), 256, split_k=split,
@@ -329,7 +338,9 @@ def splitk(torch, vk, stream, steps):
                 tf = 2.0 * 256 * 256 * K / (med * 1e-3) / 1e12
                 gbs = (A.numel() + B.numel()) * A.element_size() / (med * 1e-3) / 1e9
                 key = f"K{K}_{dt}_s{split}" if split else f"K{K}_{dt}_auto"
-                out[key] = {"ms": round(med, 4), "tflops": round(tf, 2), "GBps": round(gbs, 1)}
+                out[key] = {"ms": round(med, 4), "tflops": round(tf, 2), "GBps": round(gbs, 1),
+                            "frac_of_mfma": round(tf / (PEAK_FP16_TFLOPS if dt == "f16" else PEAK_FP32_TFLOPS), 4),
+                            "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 4)}
                 if not split:
                     pl = vk.plan(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256)
                     out[key]["split"] = pl.split
