@@ -84,16 +84,18 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     const uint32_t grid = (uint32_t)grid64;
     const bool ak = a->a_kmajor != 0, bk = a->b_kmajor != 0;
     {
-        // software-pipelined kernel for full 256x256 tiles (and split-K
-        // pass 1 on them).  K and the split-K slice a multiple of two K steps
-        // (128 bytes each): the loop runs pairs.  Buffer offsets are signed
-        // 32-bit: bound the byte span of each operand tile.
+        // software-pipelined kernel for full 256x256 tiles, and 128x128 ones
+        // for 16-bit types (also split-K pass 1 on them).  K and the split-K
+        // slice a multiple of two K steps (128 bytes each): the loop runs
+        // pairs.  Buffer offsets are signed 32-bit: bound the byte span of
+        // each operand tile.
         constexpr uint64_t ES = sizeof(T);
         constexpr uint32_t KPAIR = 256 / sizeof(T);
-        const uint64_t span_a = ((uint64_t)(a->a_kmajor ? 256 : a->K) * (uint64_t)a->lda + a->K) * ES;
-        const uint64_t span_b = ((uint64_t)(a->b_kmajor ? 256 : a->K) * (uint64_t)a->ldb + a->K) * ES;
-        if (tile == VKB_TILE_256 && full && (p.split == 1 || p.kps % KPAIR == 0) && !a->generic_only &&
-            a->K % KPAIR == 0 && span_a < (1ull << 31) && span_b < (1ull << 31)) {
+        const uint64_t span_a = ((uint64_t)(a->a_kmajor ? bm : a->K) * (uint64_t)a->lda + a->K) * ES;
+        const uint64_t span_b = ((uint64_t)(a->b_kmajor ? bn : a->K) * (uint64_t)a->ldb + a->K) * ES;
+        const bool pipe_ok = full && (p.split == 1 || p.kps % KPAIR == 0) && !a->generic_only &&
+                             a->K % KPAIR == 0 && span_a < (1ull << 31) && span_b < (1ull << 31);
+        if (tile == VKB_TILE_256 && pipe_ok) {
             if (ak) {
                 if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true>), dim3(grid), dim3(256), 0, st, p);
                 else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false>), dim3(grid), dim3(256), 0, st, p);
@@ -102,6 +104,19 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
                 else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false>), dim3(grid), dim3(256), 0, st, p);
             }
             return (int)hipGetLastError();
+        }
+        if constexpr (sizeof(T) == 2) {
+            // 16-bit 128x128 tiles: the pipelined kernel with 64x64 wave tiles
+            if (tile == VKB_TILE_128 && pipe_ok) {
+                if (ak) {
+                    if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64>), dim3(grid), dim3(256), 0, st, p);
+                    else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64>), dim3(grid), dim3(256), 0, st, p);
+                } else {
+                    if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, true, 64>), dim3(grid), dim3(256), 0, st, p);
+                    else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false, 64>), dim3(grid), dim3(256), 0, st, p);
+                }
+                return (int)hipGetLastError();
+            }
         }
     }
     switch (tile) {

@@ -1,15 +1,17 @@
-// gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp32, fp16 and bf16.
+// gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp32, fp16 and
+// bf16, and its 128x128 form for 16-bit types.
 //
-// Used for full tiles (M, N multiples of 256, K a multiple of two K steps,
-// aligned operands), also as split-K pass 1 (one K slice per workgroup row
-// of the grid, raw fp32 sums); edges and small shapes use gemm_kernel<> in
+// Used for full tiles (M, N multiples of the tile, K a multiple of two K
+// steps, aligned operands), also as split-K pass 1 (one K slice per workgroup
+// row of the grid, raw fp32 sums); edges and small shapes use gemm_kernel<> in
 // gemm_mfma.hpp, whose MFMA role swap and epilogue this kernel shares.
 // Replaces the reference's large tiles (gemm_f32_128x128_bankfree_tmpl.comp,
 // gemm_half_128x256_bankfree_tmpl.comp, gemm_half_128x128_bankfree_tmpl.comp,
 // dispatched from src/vkblas.c:1191-1313, 1822-1868).
 //
-// Per workgroup: 4 waves, 2x2, each owning a 128x128 block of C held in 256
-// AGPRs.  A K step is 128 bytes of K (64 fp16 / bf16 or 32 fp32):
+// Per workgroup: 4 waves, 2x2, each owning a WT x WT block of C (WT = 128:
+// 256 AGPRs; WT = 64: 64 AGPRs, two workgroups per CU).  A K step is 128
+// bytes of K (64 fp16 / bf16 or 32 fp32):
 //  * 16-bit types, every layout: two sub-steps of v_mfma_f32_16x16x32 on 8x8
 //    16x16 tiles (64 MFMAs each; lane group g = lane / 16 takes k 8g..8g+7 of
 //    the sub-step's 32);
@@ -80,15 +82,43 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 #define VKB_PIPE_DMA_UNITS 16
 #endif
 
-template <typename T, typename TC, bool AK, bool BKM>
-__global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
+// Read order of the SH 0 fragments of a sub-step: units in order, each
+// needing B_j (its MFMAs' columns) then A_i (its row) on first use.
+struct RdSeq {
+    int n;
+    signed char isA[16], fi[16];
+};
+template <int NF>
+constexpr RdSeq make_rdseq() {
+    RdSeq r{};
+    bool seenA[8] = {}, seenB[8] = {};
+    constexpr int MPU = NF * NF / 16;   // MFMAs per unit
+    for (int q = 0; q < 16; ++q) {
+        const int t0 = q * MPU, i = t0 / NF, j0 = t0 % NF;
+        for (int j = j0; j < j0 + MPU; ++j)
+            if (!seenB[j]) { seenB[j] = true; r.isA[r.n] = 0; r.fi[r.n] = (signed char)j; ++r.n; }
+        if (!seenA[i]) { seenA[i] = true; r.isA[r.n] = 1; r.fi[r.n] = (signed char)i; ++r.n; }
+    }
+    return r;
+}
+
+// WT: wave tile edge.  128: 256x256 workgroup tile, one workgroup per CU;
+// 64 (16-bit types): 128x128 workgroup tile for shapes with too few 256x256
+// tiles to fill the chip, two workgroups per CU.
+template <typename T, typename TC, bool AK, bool BKM, int WT = 128>
+__global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KParams p) {
     constexpr bool F16 = sizeof(T) == 2;
+    static_assert(WT == 128 || (WT == 64 && F16), "128x128 tiles are 16-bit only");
     constexpr int ES = sizeof(T);                   // element bytes
-    constexpr int BM = 256, BN = 256, BK = 128 / ES;
+    constexpr int BM = 2 * WT, BN = 2 * WT, BK = 128 / ES;
     constexpr int VEC = 16 / ES;                    // elements per 16-byte chunk
-    constexpr int A0 = 0, B0 = 4608, STG = 2304;    // u32x4 offsets
+    constexpr int NDMA = BM / 32;                   // DMA instructions per operand, wave and K step
+    constexpr int CPR = BM / 8;                     // 16-byte chunks of an MN-major k row
+    constexpr int RPB = 64 / CPR;                   // k rows per 1-KiB transposed-read block
+    constexpr int STG = (BM / 8) * 72;              // stage size (u32x4), every layout fits
+    constexpr int A0 = 0, B0 = 2 * STG;             // u32x4 offsets
     constexpr int GRP = F16 ? 64 : 72;              // 8-row group stride of K-major tiles
-    __shared__ u32x4 lds[9216];                     // 144 KB
+    __shared__ u32x4 lds[4 * STG];                  // 144 KB (BM 256) / 72 KB (BM 128)
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -130,26 +160,31 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     const int nkt = (int)(klen / BK);
 
     // K-major direct loads: instruction i of this wave fills the 8-row group
-    // 8 wave + i (rows 64 wave + 8 i + [0, 8); lane -> row + lane / 8, slot
-    // lane % 8).  With the K-major swizzle c ^ (r & 7) that slot holds chunk
-    // (lane % 8) ^ (lane / 8) for every i, so one VGPR offset serves all
-    // eight instructions; the row step 8 i and k0 go in soffset.
+    // NDMA wave + i (rows (BM / 4) wave + 8 i + [0, 8); lane -> row + lane / 8,
+    // slot lane % 8).  With the K-major swizzle c ^ (r & 7) that slot holds
+    // chunk (lane % 8) ^ (lane / 8) for every i, so one VGPR offset serves
+    // every instruction; the row step 8 i and k0 go in soffset.
     const int koff = ((lane & 7) ^ (lane >> 3)) << 4;
-    const int a_voff = (64 * wave + (lane >> 3)) * lda * ES + koff;
-    const int b_voff = (64 * wave + (lane >> 3)) * ldb * ES + koff;
+    const int a_voff = ((BM / 4) * wave + (lane >> 3)) * lda * ES + koff;
+    const int b_voff = ((BN / 4) * wave + (lane >> 3)) * ldb * ES + koff;
     // 16-bit MN-major direct loads: instruction n of this wave fills the
-    // 1-KiB block 8 wave + n (k rows 2 (8 wave + n) + [0, 2); lane -> row +
-    // lane / 32, slot lane % 32, which holds chunk (lane % 32) ^ t(row)).
-    // t(row) depends on n only through n & 1 and n >> 2, so four VGPR offsets
-    // serve the eight instructions; the row step and k0 go in soffset.
+    // 1-KiB block NDMA wave + n (k rows RPB (NDMA wave + n) + [0, RPB); lane ->
+    // row + lane / CPR, slot lane % CPR, which holds chunk
+    // (lane % CPR) ^ t(row)).  t(row) depends on n only through n & 1 and
+    // n >> 2 (BM 256) or n >> 1 (BM 128), so four or two VGPR offsets serve
+    // the instructions; the row step and k0 go in soffset.
     constexpr bool ATR = F16 && !AK, BTR = F16 && !BKM;
     auto tsw = [](int k) { return 2 * (k & 3) + 8 * (((k >> 3) ^ (k >> 4)) & 1); };
-    int a_tr[4], b_tr[4];
+    constexpr int NTRV = WT == 128 ? 4 : 2;
+    auto trv = [](int n) { return WT == 128 ? ((n & 1) | ((n >> 2) << 1)) : ((n >> 1) & 1); };
+    int a_tr[NTRV], b_tr[NTRV];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        const int k = 2 * (8 * wave + ((v & 1) | ((v >> 1) << 2))) + h;
-        a_tr[v] = h * lda * ES + (((lane & 31) ^ tsw(k)) << 4);
-        b_tr[v] = h * ldb * ES + (((lane & 31) ^ tsw(k)) << 4);
+    for (int v = 0; v < NTRV; ++v) {
+        const int n = WT == 128 ? ((v & 1) | ((v >> 1) << 2)) : 2 * v;   // an instruction of variant v
+        const int r = lane / CPR;
+        const int k = RPB * (NDMA * wave + n) + r;
+        a_tr[v] = r * lda * ES + (((lane % CPR) ^ tsw(k)) << 4);
+        b_tr[v] = r * ldb * ES + (((lane % CPR) ^ tsw(k)) << 4);
     }
     // MN-major staged loads: VECxVEC blocks (kb, mb + 32 blk), kb = tid / 32
     // (k rows kb*VEC..), mb = tid % 32 (columns (mb + 32 blk)*VEC..)
@@ -195,22 +230,23 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? ra : rb, dst, 16, voff, soff, 0, 0);
         }
     };
-    // Direct (DMA) load n of K step kt (8 per operand per wave: A then B)
+    // Direct (DMA) load n of K step kt (NDMA per operand per wave: A then B)
+    constexpr int ND = 2 * NDMA;
     auto dma_load = [&](int kt, int S, int n) {
         const int k0 = kt * BK;
-        if (n < 8) {
+        if (n < NDMA) {
             if constexpr (AK)
-                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (8 * wave + n) * GRP], a_voff, (k0 + n * 8 * lda) * ES);
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * GRP], a_voff, (k0 + n * 8 * lda) * ES);
             else if constexpr (ATR)
-                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (8 * wave + n) * 64], a_tr[(n & 1) | ((n >> 2) << 1)],
-                    (k0 + 2 * (8 * wave + n)) * lda * ES);
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * 64], a_tr[trv(n)],
+                    (k0 + RPB * (NDMA * wave + n)) * lda * ES);
         } else {
-            const int m = n - 8;
+            const int m = n - NDMA;
             if constexpr (BKM)
-                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (8 * wave + m) * GRP], b_voff, (k0 + m * 8 * ldb) * ES);
+                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (NDMA * wave + m) * GRP], b_voff, (k0 + m * 8 * ldb) * ES);
             else if constexpr (BTR)
-                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (8 * wave + m) * 64], b_tr[(m & 1) | ((m >> 2) << 1)],
-                    (k0 + 2 * (8 * wave + m)) * ldb * ES);
+                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (NDMA * wave + m) * 64], b_tr[trv(m)],
+                    (k0 + RPB * (NDMA * wave + m)) * ldb * ES);
         }
     };
     // MN-major staged load v of K step kt (8 per operand)
@@ -233,7 +269,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     // ---- MFMA shape --------------------------------------------------------
     // SH 0, 16-bit types: v_mfma_f32_16x16x32; a sub-step is one 32-wide k
     //   slice (lane group g = lane / 16 holds 8 k of row lane % 16); the
-    //   wave's 128x128 block is 8x8 tiles of 16x16 (floatx4).  With random
+    //   wave's WT x WT block is NF x NF tiles of 16x16 (floatx4).  With random
     //   data gfx950 sustains ~15% more fp16 FLOP/s on 16x16x32 than on
     //   32x32x16 (half the accumulator traffic per FLOP under the power limit).
     // SH 2, fp32: v_mfma_f32_32x32x2_f32, sub-step s = chunk 4h + s (one MFMA
@@ -241,7 +277,8 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     constexpr int SH = F16 ? 0 : 2;
     constexpr int NSUB = SH == 0 ? 2 : 4;           // sub-steps per K step
     constexpr int UPS = 32 / NSUB;                  // units per sub-step
-    constexpr int NF = SH == 0 ? 8 : 4;             // fragments per operand
+    constexpr int NF = SH == 0 ? WT / 16 : 4;       // fragments per operand
+    constexpr int MPU = NF * NF / 16;               // MFMAs per unit (SH 0)
     constexpr int FR = SH == 0 ? 16 : 32;           // rows per fragment
     constexpr int SX = SH == 0 ? 4 : 1;             // sub-step slot offset
     const int fl = SH == 0 ? (lane & 15) : l32;     // fragment row of this lane
@@ -263,7 +300,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     auto dsw = [](bool kmajor, int i) { return kmajor ? 0 : ((FR / 8) * i) & 7; };
     int xa[8], xb[8];   // indexed by the slot XOR; unused entries are dead code
     {
-        const int ra = wm * 128 + fl, rb = wn * 128 + fl;
+        const int ra = wm * WT + fl, rb = wn * WT + fl;
         const int a0 = row_base(ra, AK), ag = hoff ^ gsw(ra, AK);
         const int b0 = row_base(rb, BKM), bg = hoff ^ gsw(rb, BKM);
 #pragma unroll
@@ -274,20 +311,23 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     }
     // Transposed-read fragments (16-bit MN-major tiles): lane q of group g
     // reads row k = 8g + (q >> 2) at columns 16 i + 4 (q & 3) .. +3 of the
-    // wave's 128; its unit is (k >> 1) 64 + (k & 1) 32 + (c ^ t(k)) with
-    // c = 16 w + 2 i + ((q >> 1) & 1) and t(k) = 2 (q >> 2) + 8 ((g ^ g >> 1)
-    // & 1) (even, below 16), plus 8 bytes for odd q.  Per fragment i that is
-    // a per-lane base with (2 i ^ t); the second read (+4 rows: +2048 bytes),
-    // the second sub-step (+32 rows: +16384 bytes) and the stage are offsets.
-    int tra[8], trb[8];   // bytes
+    // wave's WT; its unit is (k / RPB) 64 + (k % RPB) CPR + (c ^ t(k)) with
+    // c = (WT / 8) w + 2 i + ((q >> 1) & 1) and t(k) = 2 (q >> 2) +
+    // 8 ((g ^ g >> 1) & 1) (even, below 16), plus 8 bytes for odd q.  Per
+    // fragment i that is a per-lane base with ((WT / 8) w + 2 i) ^ t; the
+    // second read (+4 rows), the second sub-step (+32 rows) and the stage are
+    // offsets (TR_HALF, TR_SUB bytes).
+    constexpr int TR_HALF = (4 / RPB) * 64 * 16, TR_SUB = (32 / RPB) * 64 * 16;
+    int tra[NF], trb[NF];   // bytes
     {
         const int g = lane >> 4, q = lane & 15;
         const int tk = 2 * (q >> 2) + 8 * ((g ^ (g >> 1)) & 1);
-        const int L = (4 * g + (q >> 3)) * 64 + ((q >> 2) & 1) * 32 + ((q >> 1) & 1);
+        const int k = 8 * g + (q >> 2);
+        const int L = (k / RPB) * 64 + (k % RPB) * CPR + ((q >> 1) & 1);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            tra[i] = (A0 + L + 16 * wm + ((2 * i) ^ tk)) * 16 + (q & 1) * 8;
-            trb[i] = (B0 + L + 16 * wn + ((2 * i) ^ tk)) * 16 + (q & 1) * 8;
+        for (int i = 0; i < NF; ++i) {
+            tra[i] = (A0 + L + (((WT / 8) * wm + 2 * i) ^ tk)) * 16 + (q & 1) * 8;
+            trb[i] = (B0 + L + (((WT / 8) * wn + 2 * i) ^ tk)) * 16 + (q & 1) * 8;
         }
     }
 
@@ -303,17 +343,19 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 
     // A sub-step is UPS units; its units also read the fragments of the next
     // sub-step, in the order the next sub-step first uses them.
-    // SH 0: unit q = tiles (q/2, 4(q%2) .. +3): reads B0-B3 A0 B4-B7 A1 .. A7,
-    //   a transposed-read fragment as two reads; the NRD reads are dealt over
-    //   the 16 units in order.  With K-major A, A_i is last used by unit 2i+1
-    //   and its successor is read in that unit or a later one, so A needs one
-    //   register set; a transposed-read A (two reads each) comes earlier and
-    //   takes two, as B always does.
+    // SH 0: unit q = MPU tiles from tile q MPU (row-major over NF x NF): with
+    //   WT 128 tiles (q/2, 4(q%2) .. +3), reads B0-B3 A0 B4-B7 A1 .. A7; with
+    //   WT 64 tile (q/4, q%4), reads B0 A0 B1 B2 B3 A1 A2 A3.  A
+    //   transposed-read fragment is two reads; the NRD reads are dealt over
+    //   the 16 units in order.  With WT 128 and K-major A, A_i is last used by
+    //   unit 2i+1 and its successor is read in that unit or a later one, so A
+    //   needs one register set; otherwise A is read earlier and takes two, as
+    //   B always does.
     // SH 2: unit q = k element q/2 of the chunk on tiles (2(q%2) .. +1, 0..3):
     //   reads B0..B3 A0..A3, every fragment kept to the sub-step's end: two
     //   sets each.
-    constexpr int NAB = (SH == 0 && !ATR) ? 1 : 2;
-    constexpr int NRD = 16 + (ATR ? 8 : 0) + (BTR ? 8 : 0);   // SH 0 reads per sub-step
+    constexpr int NAB = (SH == 0 && !ATR && WT == 128) ? 1 : 2;
+    constexpr int NRD = 2 * NF + (ATR ? NF : 0) + (BTR ? NF : 0);   // SH 0 reads per sub-step
     u32x4 af[NAB][NF], bf[2][NF];
     auto tr_half = [&](u32x4& dst, int half, int byte_off) {
         const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)((char*)lds + byte_off));
@@ -323,25 +365,24 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     };
     auto frag_read = [&](int buf, int S, int s, bool isA, int fi, int half) {
         if (isA) {
-            if constexpr (ATR) tr_half(af[buf % NAB][fi], half, tra[fi] + S * STG * 16 + s * 16384 + half * 2048);
+            if constexpr (ATR) tr_half(af[buf % NAB][fi], half, tra[fi] + S * STG * 16 + s * TR_SUB + half * TR_HALF);
             else af[buf % NAB][fi] = lds[xa[dsw(AK, fi) ^ (SX * s)] + S * STG + fi * ASTEP];
         } else {
-            if constexpr (BTR) tr_half(bf[buf][fi], half, trb[fi] + S * STG * 16 + s * 16384 + half * 2048);
+            if constexpr (BTR) tr_half(bf[buf][fi], half, trb[fi] + S * STG * 16 + s * TR_SUB + half * TR_HALF);
             else bf[buf][fi] = lds[xb[dsw(BKM, fi) ^ (SX * s)] + S * STG + fi * BSTEP];
         }
     };
     auto read_one = [&](int buf, int S, int s, int q) {   // the reads of unit q
         if constexpr (SH == 0) {
-            constexpr int isA16[16] = {0, 0, 0, 0, 1, 0, 0, 0, 0, 1, 1, 1, 1, 1, 1, 1};
-            constexpr int fi16[16] = {0, 1, 2, 3, 0, 4, 5, 6, 7, 1, 2, 3, 4, 5, 6, 7};
+            constexpr RdSeq SEQ = make_rdseq<NF>();
             int o = 0;   // read index in the sub-step's sequence
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const bool tr = isA16[t] ? ATR : BTR;
+            for (int t = 0; t < SEQ.n; ++t) {
+                const bool tr = SEQ.isA[t] ? ATR : BTR;
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
                     if (half == 1 && !tr) continue;
-                    if (o * 16 >= q * NRD && o * 16 < (q + 1) * NRD) frag_read(buf, S, s, isA16[t], fi16[t], half);
+                    if (o * 16 >= q * NRD && o * 16 < (q + 1) * NRD) frag_read(buf, S, s, SEQ.isA[t], SEQ.fi[t], half);
                     ++o;
                 }
             }
@@ -351,9 +392,9 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     };
     auto mfma_unit = [&](int buf, int q) {
         if constexpr (SH == 0) {
-            const int i = q >> 1, j0 = (q & 1) * 4;
+            const int i = (q * MPU) / NF, j0 = (q * MPU) % NF;
 #pragma unroll
-            for (int j = j0; j < j0 + 4; ++j)
+            for (int j = j0; j < j0 + MPU; ++j)
                 acc[i][j] = mfma_16x16x32<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
         } else {
             const int e = q >> 1, i0 = (q & 1) * 2;
@@ -369,7 +410,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
 
     // A region (between two barriers) is 32 units: the last sub-step of K step
     // kt-1 (units [0, UPS), from registers) and the first NSUB-1 sub-steps of
-    // kt.  The 16 DMA loads of kt+1 are spread over DMA_UNITS units from the
+    // kt.  The ND DMA loads of kt+1 are spread over DMA_UNITS units from the
     // first (issued in a burst they oversubscribe the texture address unit
     // and stall the MFMA issue); staged MN-major rows of kt+1 are written in
     // units [16, 24) and the staged loads of kt+2 issued in [24, 32), after
@@ -383,8 +424,8 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
         const int span = prev ? DMA_UNITS : 24 - UPS;
         const int v = u - first;
 #pragma unroll
-        for (int n = 0; n < 16; ++n)
-            if (n * span >= v * 16 && n * span < (v + 1) * 16) dma_load(kt, S, n);
+        for (int n = 0; n < ND; ++n)
+            if (n * span >= v * ND && n * span < (v + 1) * ND) dma_load(kt, S, n);
     };
 
     // Region, stage S = K step kt:
@@ -420,7 +461,7 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
         for (int v = 0; v < 8; ++v) stage_load(0, v);
     }
 #pragma unroll
-    for (int n = 0; n < 16; ++n) dma_load(0, 0, n);
+    for (int n = 0; n < ND; ++n) dma_load(0, 0, n);
     if constexpr (STAGED) {
 #pragma unroll
         for (int v = 0; v < 8; ++v) stage_store(0, v);
@@ -477,16 +518,16 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
         // address unit then handles a line per row.  Each wave owns an LDS
         // region (the K loop's last barrier has retired every tile read) with
         // rows padded by 16 bytes: the MFMA-layout writes then fall on
-        // distinct banks and each 16-lane row read covers all 64.  fp32
-        // (512-byte rows) goes in two passes of 64 rows.
-        constexpr int ROWB = 128 * (int)sizeof(TC);          // bytes of a wave-block row
+        // distinct banks.  fp32 with WT 128 (512-byte rows) goes in two
+        // passes of 64 rows.
+        constexpr int ROWB = WT * (int)sizeof(TC);           // bytes of a wave-block row
         constexpr int STR = ROWB + 16;                       // padded LDS row stride
-        constexpr int PASSES = sizeof(TC) == 4 ? 2 : 1;
-        constexpr int PROWS = 128 / PASSES;                  // rows per pass
+        constexpr int PASSES = (sizeof(TC) == 4 && WT == 128) ? 2 : 1;
+        constexpr int PROWS = WT / PASSES;                   // rows per pass
         constexpr int LPR = ROWB / 16;                       // lanes per row on read-out
-        static_assert(4 * PROWS * STR <= 9216 * 16, "epilogue staging exceeds LDS");
+        static_assert(4 * PROWS * STR <= 4 * STG * 16, "epilogue staging exceeds LDS");
         char* wl = (char*)lds + wave * (PROWS * STR);
-        TC* cblk = Cb + (int64_t)(m0 + wm * 128) * p.ldc + (n0 + wn * 128);
+        TC* cblk = Cb + (int64_t)(m0 + wm * WT) * p.ldc + (n0 + wn * WT);
 #pragma unroll
         for (int pass = 0; pass < PASSES; ++pass) {
 #pragma unroll
@@ -519,13 +560,13 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(KParams p) {
     } else {
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
-            const int m = m0 + wm * 128 + i * FR + fl;
+            const int m = m0 + wm * WT + i * FR + fl;
             TC* crow = Cb + (int64_t)m * p.ldc;
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
-                    const int n = n0 + wn * 128 + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
+                    const int n = n0 + wn * WT + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
                     float x[4], o[4];
                     load4<TC>(crow + n, o, true);
 #pragma unroll
