@@ -12,7 +12,7 @@ import oracle
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(512, 768, 384), (256, 256, 128), (300, 520, 200), (96, 160, 72)]
+SHAPES = [(512, 768, 384), (256, 256, 128), (256, 384, 256), (300, 520, 200), (96, 160, 72)]
 VARIANTS = [(tile, generic) for tile in (0, 1, 2) for generic in (False, True) if not (generic and tile == 0)]
 
 
@@ -72,3 +72,37 @@ def test_kernel_variant(tile, generic, dt, op_a, op_b, shape, beta):
         vk.gemm_async(vk.DT_F16, vk.DT_F32, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb,
                       beta, dC.data_ptr(), ldc, split_k=1)
         assert normwise(to_host(dC), ref) <= F16_BOUND
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_pipe128_many_tiles(dt, op_a, op_b):
+    """16-bit 128x128 pipelined kernel with more workgroups than CUs (two LDS
+    stages, two workgroups per CU): 2304 x 2304 output = 324 tiles; the
+    one-workgroup-per-CU grids above take the four-stage form."""
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, BF16_BOUND
+    M, N, K = 2304, 2304, 384
+    print(f"[case] pipe128 many tiles {dt} op={op_a}{op_b}", flush=True)
+    vk.set_override(1, False)
+    lda = M if op_a else K
+    ldb = K if op_b else N
+    conv, back, bound = ((oracle.f2h_rne, oracle.h2f, F16_BOUND) if dt == "f16"
+                         else (oracle.f2bf_rne, oracle.bf2f, BF16_BOUND))
+    vdt = vk.DT_F16 if dt == "f16" else vk.DT_BF16
+    ha = conv(rng(11 + op_a, lda * (K if op_a else M)))
+    hb = conv(rng(13 + op_b, ldb * (N if op_b else K)))
+    dA, dB = to_dev(ha), to_dev(hb)
+    dC = torch.full((M * N,), float("nan"), dtype=torch.float16, device="cuda:0")
+    vk.gemm_async(vdt, vdt, op_a, op_b, M, N, K, 1.0, dA.data_ptr(), lda, dB.data_ptr(), ldb, 0.0,
+                  dC.data_ptr(), N, split_k=1)
+    got = to_host(dC)
+    rows = oracle.sample_rows(M, 12)
+    ref = np.zeros(M * N, np.uint16)
+    if dt == "f16":
+        oracle.ref_gemm_f16_rm(op_a, op_b, M, N, K, ha, lda, hb, ldb, 1.0, 0.0, ref, N, rows=rows)
+    else:
+        oracle.ref_gemm_bf16_rm(op_a, op_b, M, N, K, ha, lda, hb, ldb, 1.0, 0.0, ref, N, rows=rows)
+    sel = (rows[:, None] * N + np.arange(N)[None, :]).reshape(-1)
+    assert np.all(np.isfinite(back(got[sel])))
+    assert normwise(back(got[sel]), back(ref[sel])) <= bound

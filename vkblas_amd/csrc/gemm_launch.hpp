@@ -37,6 +37,19 @@ static int launch_layout(const KParams& p, bool ak, bool bk, bool checked, uint3
 
 static inline bool aligned(const void* ptr, uintptr_t a) { return ((uintptr_t)ptr % a) == 0; }
 
+// Compute units of the current device (cached per device; 0 if unknown).
+static inline uint32_t cu_count() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    int n = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+    if (n == 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+        __atomic_store_n(&cached[dev], n, __ATOMIC_RELAXED);
+    }
+    return (uint32_t)n;
+}
+
 template <typename T, typename TC>
 static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     constexpr int VEC = Elem<T>::VEC;
@@ -106,9 +119,19 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             return (int)hipGetLastError();
         }
         if constexpr (sizeof(T) == 2) {
-            // 16-bit 128x128 tiles: the pipelined kernel with 64x64 wave tiles
+            // 16-bit 128x128 tiles: the pipelined kernel with 64x64 wave tiles;
+            // four LDS stages when the grid is at most one workgroup per CU
+            // (the 144 KB they take allow no second one), else two
             if (tile == VKB_TILE_128 && pipe_ok) {
-                if (ak) {
+                if (grid <= cu_count()) {
+                    if (ak) {
+                        if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64, 4>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64, 4>), dim3(grid), dim3(256), 0, st, p);
+                    } else {
+                        if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, true, 64, 4>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false, 64, 4>), dim3(grid), dim3(256), 0, st, p);
+                    }
+                } else if (ak) {
                     if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64>), dim3(grid), dim3(256), 0, st, p);
                     else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64>), dim3(grid), dim3(256), 0, st, p);
                 } else {

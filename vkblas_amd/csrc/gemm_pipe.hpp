@@ -104,11 +104,16 @@ constexpr RdSeq make_rdseq() {
 
 // WT: wave tile edge.  128: 256x256 workgroup tile, one workgroup per CU;
 // 64 (16-bit types): 128x128 workgroup tile for shapes with too few 256x256
-// tiles to fill the chip, two workgroups per CU.
-template <typename T, typename TC, bool AK, bool BKM, int WT = 128>
-__global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KParams p) {
+// tiles to fill the chip.
+// NST: LDS stages.  2: the DMA of a K step is issued one step ahead.  4
+// (WT 64 only, 144 KB: one workgroup per CU, for grids of at most one
+// workgroup per CU): three steps ahead, since a 128x128 step (512 MFMA
+// cycles) is shorter than the load latency.
+template <typename T, typename TC, bool AK, bool BKM, int WT = 128, int NST = 2>
+__global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pipe_kernel(KParams p) {
     constexpr bool F16 = sizeof(T) == 2;
     static_assert(WT == 128 || (WT == 64 && F16), "128x128 tiles are 16-bit only");
+    static_assert(NST == 2 || (NST == 4 && WT == 64), "four stages only fit 128x128 tiles");
     constexpr int ES = sizeof(T);                   // element bytes
     constexpr int BM = 2 * WT, BN = 2 * WT, BK = 128 / ES;
     constexpr int VEC = 16 / ES;                    // elements per 16-byte chunk
@@ -116,9 +121,9 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
     constexpr int CPR = BM / 8;                     // 16-byte chunks of an MN-major k row
     constexpr int RPB = 64 / CPR;                   // k rows per 1-KiB transposed-read block
     constexpr int STG = (BM / 8) * 72;              // stage size (u32x4), every layout fits
-    constexpr int A0 = 0, B0 = 2 * STG;             // u32x4 offsets
+    constexpr int A0 = 0, B0 = NST * STG;           // u32x4 offsets: A stages, then B stages
     constexpr int GRP = F16 ? 64 : 72;              // 8-row group stride of K-major tiles
-    __shared__ u32x4 lds[4 * STG];                  // 144 KB (BM 256) / 72 KB (BM 128)
+    __shared__ u32x4 lds[2 * NST * STG];            // 144 KB (BM 256; BM 128 x 4 stages) / 72 KB
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -208,14 +213,16 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
     // staged registers: index blk * VEC + k row within the block
     u32x4 sa_v[(STAGED && !AK) ? 8 : 1], sb_v[(STAGED && !BKM) ? 8 : 1];
 
-    // With a transposed-read operand every DMA is issued as inline assembly.
-    // The compiler waits for all LDS DMA in flight (vmcnt) before each
-    // ds_read_b64_tr_b16 it emits, which would serialize the loads behind the
-    // reads; as assembly the DMA is outside its wait-count tracking.  The
-    // end-of-step "s_waitcnt vmcnt(0)" + barrier (sync_vm) is what orders a
-    // step's DMA before any read of its stage, and these kernels have no
-    // other vector-memory load in flight in the K loop.
-    constexpr bool ASM_DMA = ATR || BTR;
+    // With a transposed-read operand or more than two stages every DMA is
+    // issued as inline assembly.  The compiler waits for all LDS DMA in
+    // flight (vmcnt) before each ds_read_b64_tr_b16 it emits, which would
+    // serialize the loads behind the reads, and it cannot tell which stage a
+    // DMA writes; as assembly the DMA is outside its wait-count tracking.
+    // The end-of-step "s_waitcnt vmcnt(n)" + barrier (sync_vm) is what orders
+    // a step's DMA before any read of its stage (n counts the DMA of later
+    // steps, issued after it: vector loads complete in order), and these
+    // kernels have no other vector-memory load in flight in the K loop.
+    constexpr bool ASM_DMA = ATR || BTR || NST > 2;
     auto rsrc_words = [](const void* base) {
         const uint64_t a = (uint64_t)base;
         return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
@@ -438,7 +445,9 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
     // Sub-step s of K step kt uses fragment buffer s & 1 (NSUB is even).
     // Every unit (MFMAs + companions) is fenced with sched_barrier so the
     // compiler keeps this order and both fragment sets live.
-    auto region = [&](int kt, int S, bool prev, bool next, bool next2) {
+    // next: this region issues the DMA of step kt + NST - 1 (into the stage
+    // step kt - 1 used); wc: the vmcnt that leaves step kt + 1 landed.
+    auto region = [&](int kt, int S, bool prev, bool next, bool next2, auto wc) {
 #pragma unroll
         for (int u = prev ? 0 : UPS; u < 32; ++u) {
             const int sub = u / UPS - 1;          // sub-step of kt run here (-1: kt-1's last)
@@ -446,15 +455,15 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
             const int buf = sub < 0 ? (NSUB - 1) & 1 : sub & 1;
             mfma_unit(buf, q);
             read_one((sub + 1) & 1, S, sub + 1, q);
-            if (next) dma_unit(kt + 1, S ^ 1, u, prev);
+            if (next) dma_unit(kt + NST - 1, (S + NST - 1) % NST, u, prev);
             if (STAGED && next && u >= 16 && u < 24) stage_store(S ^ 1, u - 16);
             if (STAGED && next2 && u >= 24) stage_load(kt + 2, u - 24);
             __builtin_amdgcn_sched_barrier(0);
         }
-        // DMA of kt+1 landed (staged loads of kt+2 may still fly)
-        if (next && next2) sync_vm(std::integral_constant<int, NSTAGED>{});
-        else sync_vm(std::integral_constant<int, 0>{});
+        sync_vm(wc);
     };
+    using W0 = std::integral_constant<int, 0>;
+    using WS = std::integral_constant<int, NSTAGED>;   // staged loads of kt+2 may still fly
 
     // ---- prologue: K step 0 into stage 0 (and staged rows of step 1) ----
     if constexpr (STAGED) {
@@ -464,23 +473,51 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
     }
 #pragma unroll
     for (int n = 0; n < ND; ++n) dma_load(0, 0, n);
-    if constexpr (STAGED) {
+    if constexpr (NST == 4) {
+        // steps 1 and 2 as well (nkt >= 4), or step 1 only (nkt == 2)
 #pragma unroll
-        for (int v = 0; v < 8; ++v) stage_store(0, v);
+        for (int n = 0; n < ND; ++n) dma_load(1, 1, n);
+        if (nkt > 2) {
 #pragma unroll
-        for (int v = 0; v < 8; ++v) stage_load(1, v);   // nkt >= 2
+            for (int n = 0; n < ND; ++n) dma_load(2, 2, n);
+            sync_vm(std::integral_constant<int, 2 * ND>{});
+        } else {
+            sync_vm(std::integral_constant<int, ND>{});
+        }
+    } else {
+        if constexpr (STAGED) {
+#pragma unroll
+            for (int v = 0; v < 8; ++v) stage_store(0, v);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) stage_load(1, v);   // nkt >= 2
+        }
+        sync_vm(WS{});
     }
-    sync_vm(std::integral_constant<int, NSTAGED>{});
 #pragma unroll
     for (int q = 0; q < UPS; ++q) read_one(0, 0, 0, q);
 
-    // nkt is even: regions alternate stages 0 and 1; the loop body is
-    // branch-free, the last two regions load less
-    if (nkt == 2) {
-        region(0, 0, false, true, false);
-        region(1, 1, true, false, false);
+    // nkt is even: regions cycle through the stages; the loop body is
+    // branch-free, the last regions load less
+    if constexpr (NST == 4) {
+        using W1 = std::integral_constant<int, ND>;
+        using W2 = std::integral_constant<int, 2 * ND>;
+        if (nkt == 2) {
+            region(0, 0, false, false, false, W0{});
+            region(1, 1, true, false, false, W0{});
+        } else {
+            region(0, 0, false, true, false, W2{});   // loads step 3
+            int kt = 1;
+#pragma clang loop unroll(disable)
+            for (; kt + 3 < nkt; ++kt) region(kt, kt & 3, true, true, false, W2{});
+            region(kt, kt & 3, true, false, false, W1{});             // kt == nkt - 3
+            region(kt + 1, (kt + 1) & 3, true, false, false, W0{});
+            region(kt + 2, (kt + 2) & 3, true, false, false, W0{});
+        }
+    } else if (nkt == 2) {
+        region(0, 0, false, true, false, W0{});
+        region(1, 1, true, false, false, W0{});
     } else {
-        region(0, 0, false, true, true);
+        region(0, 0, false, true, true, WS{});
         int kt = 1;
         if constexpr (SH == 0) {
             // One region per iteration, stage from the loop counter: with two
@@ -491,17 +528,17 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
             // keeps the constant stages: its staged stores' addresses fold
             // into immediates, and it shows no such copies.
 #pragma clang loop unroll(disable)
-            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, true);
-            region(kt, kt & 1, true, true, false);             // kt == nkt - 2: loads step nkt-1
-            region(kt + 1, (kt + 1) & 1, true, false, false);
+            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, true, WS{});
+            region(kt, kt & 1, true, true, false, W0{});             // kt == nkt - 2: loads step nkt-1
+            region(kt + 1, (kt + 1) & 1, true, false, false, W0{});
         } else {
             for (; kt + 3 < nkt; kt += 2) {
-                region(kt, 1, true, true, true);
-                region(kt + 1, 0, true, true, true);
+                region(kt, 1, true, true, true, WS{});
+                region(kt + 1, 0, true, true, true, WS{});
             }
-            region(kt, 1, true, true, true);       // kt == nkt - 3: stages step nkt-1
-            region(kt + 1, 0, true, true, false);  // loads step nkt-1
-            region(kt + 2, 1, true, false, false);
+            region(kt, 1, true, true, true, WS{});       // kt == nkt - 3: stages step nkt-1
+            region(kt + 1, 0, true, true, false, W0{});  // loads step nkt-1
+            region(kt + 2, 1, true, false, false, W0{});
         }
     }
 #pragma unroll
@@ -530,7 +567,7 @@ __global__ __launch_bounds__(256, WT == 128 ? 1 : 2) void gemm_pipe_kernel(KPara
         constexpr int PASSES = (sizeof(TC) == 4 && WT == 128) ? 2 : 1;
         constexpr int PROWS = WT / PASSES;                   // rows per pass
         constexpr int LPR = ROWB / 16;                       // lanes per row on read-out
-        static_assert(4 * PROWS * STR <= 4 * STG * 16, "epilogue staging exceeds LDS");
+        static_assert(4 * PROWS * STR <= 2 * NST * STG * 16, "epilogue staging exceeds LDS");
         char* wl = (char*)lds + wave * (PROWS * STR);
         TC* cblk = Cb + (int64_t)(m0 + wm * WT) * p.ldc + (n0 + wn * WT);
 #pragma unroll
