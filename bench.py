@@ -276,9 +276,6 @@ def main():
                      "algorithmic": "2*4096^3 FLOP per launch"},
         "tflops_by_variant": h["tflops_by_variant"],
     }
-    if not args.no_cpu:
-        log("[bench] cpu baseline")
-        line["cpu_baseline"] = cpu_baseline()
     log("[bench] fp16 4096^3")
     line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps)
     log("[bench] fp16 matvec 8192x8192")
@@ -296,6 +293,10 @@ def main():
     log("[bench] split-K and strided-batched")
     line["splitk_256x256"] = splitk(torch, vk, stream, args.steps, splits=(0,))
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
+    if not args.no_cpu:
+        # last, so the GPU legs run back to back without an idle gap between them
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
 
 
