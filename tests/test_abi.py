@@ -150,8 +150,9 @@ def test_plan_split_heuristic_and_off():
     assert pl.path == vk.PATH_SPLITK and 2 <= pl.split <= 256
     # whole 256x256 tiles: pass 1 on the pipelined kernel, slices of whole K-step pairs
     assert pl.tile == 2 and pl.k_per_split % 64 == 0
+    # 16-bit inputs: 128x128 tiles, about a workgroup per CU
     pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 262144, 262144, 256, 256)
-    assert pl.path == vk.PATH_SPLITK and pl.tile == 2 and pl.k_per_split % 128 == 0
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 128 == 0 and 4 * pl.split <= 256
     # ragged M: the 128x128 generic split
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1

@@ -229,11 +229,12 @@ def test_splitk(K, dtype, split):
 @pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("mode", ["auto", "ragged"])
 def test_splitk_pipelined(dtype, op_a, op_b, mode):
-    """Split-K pass 1 on the pipelined 256x256 kernel, every layout.
-    auto: the planner's choice at M = N = 256, K = 16384 (a slice per CU,
-    alpha = 1, beta = 0, 16-bit output for 16-bit inputs); ragged: tile forced
-    to 256, a 256 x 512 output, split 7 over K = 8448 (the last slice
-    shorter), alpha / beta on an fp32 C.  Bitwise reproducible run to run."""
+    """Split-K pass 1 on the pipelined kernel, every layout.  auto: the
+    planner's choice at M = N = 256, K = 16384 (256x256 tiles for fp32,
+    128x128 four-stage tiles for 16-bit inputs; alpha = 1, beta = 0, 16-bit
+    output for 16-bit inputs); ragged: tile forced to 256, a 256 x 512
+    output, split 7 over K = 8448 (the last slice shorter), alpha / beta on an
+    fp32 C.  Bitwise reproducible run to run."""
     import vkblas_amd as vk
     from gpu_helpers import to_dev, to_host, normwise, f32_bound, F16_BOUND, BF16_BOUND
     auto = mode == "auto"
@@ -255,11 +256,14 @@ def test_splitk_pipelined(dtype, op_a, op_b, mode):
         vk.set_override(2, False)
     try:
         pl = vk.plan(dt, ct, op_a, op_b, M, N, K, lda, ldb, N, split_k=0 if auto else 7)
-        assert pl.path == vk.PATH_SPLITK and pl.tile == 2
+        # the planner: 256x256 tiles for fp32, 128x128 (four-stage pass 1) for 16-bit inputs
+        tile = 1 if (auto and dtype != "f32") else 2
+        assert pl.path == vk.PATH_SPLITK and pl.tile == tile
         step2 = 64 if dtype == "f32" else 128
         assert pl.k_per_split % step2 == 0 and (K - (pl.split - 1) * pl.k_per_split) % step2 == 0
         if auto:
-            assert pl.split * (M // 256) * (N // 256) >= 64
+            edge = 64 << tile
+            assert pl.split * (M // edge) * (N // edge) >= 64
         else:
             assert K - (pl.split - 1) * pl.k_per_split < pl.k_per_split
         dA, dB = to_dev(hA), to_dev(hB)
