@@ -12,7 +12,7 @@ fp16 MFMA peak, 8192x8192 fp16 decode matvec vs HBM peak, with three weight
 copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched|ceiling]
 """
 import argparse
 import json
@@ -169,6 +169,34 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
     return out
 
 
+def mfma_ceiling(torch, vk, stream, steps):
+    """The v_mfma_f32_16x16x32 rate the chip sustains with no memory traffic
+    (vkblas_mfma_probe: the GEMM inner loop's MFMA pattern without its loads),
+    on operands drawn as the 16-bit legs' data (N(0,1)/sqrt(4096)) and on
+    zeros.  Under the power limit this rate depends on the data; it is the
+    ceiling the 16-bit GEMM legs' frac_of_peak is held to."""
+    sp = stream.cuda_stream
+    blocks, iters = 256, 320                     # 172 GFLOP a launch, as long as a 4096^3 GEMM
+    flops = blocks * 4 * iters * 32 * 16 * 16 * 32 * 2
+    out = torch.empty(blocks * 256, device="cuda:0")
+    g = torch.Generator(device="cuda:0").manual_seed(13)
+    res = {}
+    for name, bf16 in (("fp16", False), ("bf16", True)):
+        dt = torch.bfloat16 if bf16 else torch.float16
+        for data in ("normal", "zeros"):
+            ops = torch.randn(12 * 64 * 8, device="cuda:0", generator=g) / 64.0
+            ops = (ops if data == "normal" else torch.zeros_like(ops)).to(dt)
+
+            def call(i):
+                vk.mfma_probe(bf16, ops.data_ptr(), out.data_ptr(), blocks, iters, stream=sp)
+            for i in range(3):
+                call(i)
+            med = batch_ms(torch, stream, call, max(steps, 20))
+            tf = flops / (med * 1e-3) / 1e12
+            res[f"{name}_{data}"] = {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's CPU GEMM (test/test_gemm.c:32-58, restated in
     oracle/ref_gemm.c) on the headline workload, NN, parallel over output
@@ -207,7 +235,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "splitk", "batched", "calibrate"],
+    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "splitk", "batched", "calibrate",
+                                       "ceiling"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -238,6 +267,9 @@ def main():
         return
     if args.only == "batched":
         print(json.dumps(batched(torch, vk, stream, args.steps)))
+        return
+    if args.only == "ceiling":
+        print(json.dumps(mfma_ceiling(torch, vk, stream, args.steps)))
         return
     if args.only == "calibrate":
         print(json.dumps(calibrate(torch, stream)))
@@ -278,6 +310,8 @@ def main():
     }
     log("[bench] fp16 4096^3")
     line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps)
+    log("[bench] MFMA rate without memory traffic (power-limited ceiling of the 16-bit legs)")
+    line["mfma_ceiling"] = mfma_ceiling(torch, vk, stream, args.steps)
     log("[bench] fp16 matvec 8192x8192")
     line["fp16_matvec_8192"] = matvec(torch, vk, stream, args.steps)
     log("[bench] bf16 4096^3")

@@ -114,6 +114,18 @@ int vkblas_last_path(void);
 /* Library version string. */
 const char* vkblas_version(void);
 
+/* MFMA rate probe (no counterpart in the reference; a measurement, not a
+ * GEMM).  Launches `blocks` workgroups of four waves on `stream`; every wave
+ * reads twelve 16x16x32 operand fragments once from `operands` (12 x 64
+ * 16-byte units, fp16 or, with bf16 != 0, bf16 bit patterns) and issues
+ * `iters` x 32 independent v_mfma_f32_16x16x32 with no memory traffic, then
+ * writes one float per thread to `out` (blocks x 256 floats).  FLOPs per
+ * launch: blocks x 4 x iters x 32 x 16384.  bench.py uses it to measure the
+ * matrix rate the chip sustains under its power limit for given data.
+ * Returns 0 or a HIP error code (bad sizes, misaligned pointers). */
+int vkblas_mfma_probe(int bf16, const void* operands, float* out, uint32_t blocks, uint32_t iters,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

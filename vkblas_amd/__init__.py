@@ -86,6 +86,8 @@ def load():
     L.vkblas_version.restype = ctypes.c_char_p
     L.vkblas_cache_invalidate_base.argtypes = [_vp]
     L.vkblas_cache_invalidate_base.restype = None
+    L.vkblas_mfma_probe.argtypes = [_int, _vp, _vp, _u32, _u32, _vp]
+    L.vkblas_mfma_probe.restype = _int
     _lib = L
     return L
 
@@ -112,6 +114,14 @@ def set_override(tile: int = -1, generic: bool = False) -> None:
 
 def last_path() -> int:
     return load().vkblas_last_path()
+
+
+def mfma_probe(bf16, operands, out, blocks, iters, stream=None) -> None:
+    """vkblas_mfma_probe: blocks x 4 waves x iters x 32 v_mfma_f32_16x16x32 on
+    the twelve fragments at `operands` (device pointer), no memory traffic."""
+    st = load().vkblas_mfma_probe(1 if bf16 else 0, operands, out, blocks, iters, stream)
+    if st != 0:
+        raise RuntimeError(f"vkblas_mfma_probe: HIP error {st}")
 
 
 def gemm_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1,

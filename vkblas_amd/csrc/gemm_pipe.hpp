@@ -426,7 +426,10 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // every DMA, which the end-of-region wait relies on.  The first region
     // has no previous sub-step: its units start at UPS and its DMA is spread
     // over [UPS, 24).
-    constexpr int DMA_UNITS = VKB_PIPE_DMA_UNITS;
+    // 16-bit 256x256 tiles with K-major A and transposed-read B: 24 units
+    // (fp16 4096^3 -4%, 8192^3 -1%; the same spread costs the K-major /
+    // K-major form 2-3% at 8192^3, and 20 units change neither).
+    constexpr int DMA_UNITS = (F16 && WT == 128 && AK && !BKM) ? 24 : VKB_PIPE_DMA_UNITS;
     static_assert(DMA_UNITS >= 1 && DMA_UNITS <= 24, "the DMA must precede the staged loads of unit 24");
     auto dma_unit = [&](int kt, int S, int u, bool prev) {   // u: unit of the region
         const int first = prev ? 0 : UPS;
