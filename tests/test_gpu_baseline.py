@@ -320,6 +320,43 @@ def test_splitk_fp16_out_alpha_beta(trans):
     assert normwise(oracle.h2f(to_host(dC)), oracle.h2f(ref)) <= F16_BOUND
 
 
+def test_splitk_workspace_per_stream():
+    """Split-K partials live in a workspace kept per stream.  Calls queued on
+    two streams with no synchronisation in between, each stream's later calls
+    needing more partials than its earlier ones (the workspace grows while
+    earlier calls are still queued), every call made twice: each result
+    matches the oracle and the two runs of a call are bitwise equal."""
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, f32_bound
+    print("[case] splitk workspace, two streams", flush=True)
+    cases = [(64, 64, 8192, 8), (128, 128, 8192, 16), (256, 256, 8192, 32), (128, 256, 16384, 64)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    jobs = []
+    for si in range(2):
+        for ci, (M, N, K, split) in enumerate(cases):
+            a = rng_uniform(500 + 10 * si + ci, M * K)
+            b = rng_uniform(600 + 10 * si + ci, K * N)
+            outs = [torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda:0") for _ in range(2)]
+            jobs.append((streams[si], M, N, K, split, a, b, to_dev(a), to_dev(b), outs))
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for ci in range(len(cases)):
+            for si in range(2):
+                st, M, N, K, split, _, _, dA, dB, outs = jobs[si * len(cases) + ci]
+                vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, vk.OP_N, M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(),
+                              N, 0.0, outs[rep].data_ptr(), N, split_k=split, stream=st.cuda_stream)
+                assert vk.last_path() == vk.PATH_SPLITK
+    torch.cuda.synchronize()
+    for st, M, N, K, split, a, b, _, _, outs in jobs:
+        h0, h1 = to_host(outs[0]), to_host(outs[1])
+        assert np.array_equal(h0.view(np.uint32), h1.view(np.uint32))
+        rows = oracle.sample_rows(M, 12)
+        ref = np.zeros(M * N, np.float32)
+        oracle.ref_gemm_f32_rm(0, 0, M, N, K, a, K, b, N, 1.0, 0.0, ref, N, rows=rows)
+        sel = (rows[:, None] * N + np.arange(N)[None, :]).reshape(-1)
+        assert normwise(h0[sel], ref[sel]) <= f32_bound(K)
+
+
 # ----------------------------------------------------------------- config 5b
 
 def test_strided_batched_64x512(handle):

@@ -10,8 +10,9 @@
  *
  * Differences by design:
  *   - no global lock: the only shared state is initialised once
- *     (pthread_once) and the split-K workspace comes from a stream-ordered
- *     memory pool, so concurrent calls on different streams never share it;
+ *     (pthread_once) and the split-K workspace is kept per stream (allocated
+ *     from a stream-ordered memory pool), so concurrent calls on different
+ *     streams never share it;
  *   - launches are asynchronous on the caller's stream;
  *   - every TA/TB variant runs natively (no transposed copies, no cache).
  */
@@ -88,6 +89,64 @@ static hipMemPool_t pool_for_current_device(void) {
         }
     }
     hipMemPool_t p = g_pool[dev];
+    pthread_mutex_unlock(&g_pool_lock);
+    return p;
+}
+
+/* Split-K partials: one workspace per (device, stream), kept between calls.
+ * Work on a stream runs in order, so a call reuses its stream's workspace
+ * after the kernels of the calls queued before it; calls on other streams
+ * use their own.  A stream-ordered malloc / free pair per call instead left
+ * the GPU idle for about 6 us between calls.  A call that needs more gets a
+ * new buffer of at least twice the size (up to 1 GiB); the old one is never
+ * freed, since a call on another thread may still be about to launch on it
+ * (at most the last size again per stream stays allocated until exit).
+ * When every slot is taken the call allocates and releases its own
+ * (*owned = 1: the caller frees it on the stream after its kernels). */
+#define VKB_WS_SLOTS 64
+typedef struct {
+    int dev;
+    hipStream_t stream;
+    void* ptr;
+    size_t bytes;
+} ws_slot_t;
+static ws_slot_t g_ws[VKB_WS_SLOTS];
+static int g_nws = 0;
+
+static void* stream_workspace(hipStream_t stream, size_t bytes, int* owned) {
+    *owned = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return NULL;
+    hipMemPool_t pool = pool_for_current_device();
+    if (!pool) return NULL;
+    void* p = NULL;
+    pthread_mutex_lock(&g_pool_lock);
+    int i = 0;
+    while (i < g_nws && !(g_ws[i].dev == dev && g_ws[i].stream == stream)) ++i;
+    if (i < g_nws && g_ws[i].bytes >= bytes) {
+        p = g_ws[i].ptr;
+    } else if (i < g_nws || g_nws < VKB_WS_SLOTS) {
+        size_t want = bytes;
+        if (i < g_nws) {
+            const size_t twice = g_ws[i].bytes * 2, cap = (size_t)1 << 30;
+            if (twice > want) want = twice < cap ? twice : (cap > want ? cap : want);
+        }
+        if (hipMallocFromPoolAsync(&p, want, pool, stream) != hipSuccess) {
+            p = NULL;
+        } else {
+            if (i == g_nws) {
+                g_ws[i].dev = dev;
+                g_ws[i].stream = stream;
+                ++g_nws;
+            }
+            g_ws[i].ptr = p;
+            g_ws[i].bytes = want;
+        }
+    } else if (hipMallocFromPoolAsync(&p, bytes, pool, stream) == hipSuccess) {
+        *owned = 1;
+    } else {
+        p = NULL;
+    }
     pthread_mutex_unlock(&g_pool_lock);
     return p;
 }
@@ -311,18 +370,15 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
 
     if (plan.path == VKBLAS_PATH_SKINNY && plan.split > 1) {
         /* decode with K split over workgroups: fp32 partials, fixed-order reduce */
-        hipMemPool_t pool = pool_for_current_device();
-        if (!pool) return VKBLAS_ERR_INIT;
-        void* ws = NULL;
-        if (hipMallocFromPoolAsync(&ws, (size_t)plan.split * M * N * sizeof(float), pool, (hipStream_t)stream) !=
-            hipSuccess)
-            return VKBLAS_ERR_INIT;
+        int owned = 0;
+        void* ws = stream_workspace((hipStream_t)stream, (size_t)plan.split * M * N * sizeof(float), &owned);
+        if (!ws) return VKBLAS_ERR_INIT;
         rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode, alpha_dev,
                                beta_dev, (float*)ws, plan.split, stream);
         if (rc == 0)
             rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
                                           (int)scalar_mode, alpha_dev, beta_dev, stream);
-        hipFreeAsync(ws, (hipStream_t)stream);
+        if (owned) hipFreeAsync(ws, (hipStream_t)stream);
     } else if (plan.path == VKBLAS_PATH_SKINNY) {
         rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
                                alpha_dev, beta_dev, NULL, 1, stream);
@@ -345,11 +401,9 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
         a.generic_only = g_generic_only;
         if (plan.path == VKBLAS_PATH_SPLITK) {
-            hipMemPool_t pool = pool_for_current_device();
-            if (!pool) return VKBLAS_ERR_INIT;
-            const size_t bytes = (size_t)plan.split * M * N * sizeof(float);
-            void* ws = NULL;
-            if (hipMallocFromPoolAsync(&ws, bytes, pool, (hipStream_t)stream) != hipSuccess) return VKBLAS_ERR_INIT;
+            int owned = 0;
+            void* ws = stream_workspace((hipStream_t)stream, (size_t)plan.split * M * N * sizeof(float), &owned);
+            if (!ws) return VKBLAS_ERR_INIT;
             a.C = ws;
             a.ldc = N;
             a.stride_c = 0;
@@ -364,7 +418,7 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             if (rc == 0)
                 rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct,
                                               alpha, beta, (int)scalar_mode, alpha_dev, beta_dev, stream);
-            hipFreeAsync(ws, (hipStream_t)stream);
+            if (owned) hipFreeAsync(ws, (hipStream_t)stream);
         } else {
             rc = vkb_launch_gemm(&a, plan.tile, stream);
         }
