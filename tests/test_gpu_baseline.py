@@ -357,6 +357,55 @@ def test_splitk_workspace_per_stream():
         assert normwise(h0[sel], ref[sel]) <= f32_bound(K)
 
 
+def test_splitk_workspace_threads():
+    """Host threads issuing split-K calls at once, each on its own stream
+    (the workspace table is shared, each stream's workspace is not): every
+    result equals the same call made alone, bit for bit."""
+    import threading
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host
+    print("[case] splitk workspace, four threads", flush=True)
+    M, N, K = 128, 128, 16384
+    nthreads, calls = 4, 6
+    a = [to_dev(rng_uniform(700 + t, M * K)) for t in range(nthreads)]
+    b = [to_dev(rng_uniform(710 + t, K * N)) for t in range(nthreads)]
+    splits = (4, 16, 64)
+    alone = {}
+    for t in range(nthreads):
+        for sp in splits:
+            c = torch.empty(M * N, dtype=torch.float32, device="cuda:0")
+            vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, vk.OP_N, M, N, K, 1.0, a[t].data_ptr(), K, b[t].data_ptr(),
+                          N, 0.0, c.data_ptr(), N, split_k=sp)
+            alone[t, sp] = to_host(c)
+    outs = [[torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda:0") for _ in range(calls)]
+            for _ in range(nthreads)]
+    streams = [torch.cuda.Stream() for _ in range(nthreads)]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(t):
+        try:
+            for i in range(calls):
+                # splits 4, 16, 64, 4, ...: the stream's workspace grows while
+                # its earlier calls are still queued
+                vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, vk.OP_N, M, N, K, 1.0, a[t].data_ptr(), K,
+                              b[t].data_ptr(), N, 0.0, outs[t][i].data_ptr(), N, split_k=splits[i % 3],
+                              stream=streams[t].cuda_stream)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(nthreads)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors
+    torch.cuda.synchronize()
+    for t in range(nthreads):
+        for i in range(calls):
+            assert np.array_equal(to_host(outs[t][i]).view(np.uint32), alone[t, splits[i % 3]].view(np.uint32))
+
+
 # ----------------------------------------------------------------- config 5b
 
 def test_strided_batched_64x512(handle):
