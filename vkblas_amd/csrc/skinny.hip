@@ -39,6 +39,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // Element type T of X and W (_Float16 or __bf16): the two 16-bit products.
 template <typename T>
@@ -218,6 +219,164 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkParams p) {
         float s = 0.0f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) s += red[w][r][e][src_lane];
+        TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
+        float y = alpha * s;
+        if (beta != 0.0f) y += beta * (float)*dst;
+        *dst = (TC)y;
+    }
+}
+
+// ------------------------------------------------------- staged skinny
+// For 3 <= M <= 16 activation rows, full-line loads.  skinny_kernel's loads
+// take 64 bytes of each of 16 weight rows per instruction (the MFMA fragment
+// layout); here every load is a buffer-to-LDS copy (buffer_load_dwordx4 ...
+// lds: lane l writes 16 B at M0 + 16 l) of 4 rows x 256 contiguous bytes,
+// whole 128-byte lines streamed non-temporal, and the fragments are read back
+// from LDS.
+// Workgroup: one 16-row weight tile, four waves splitting the full 128-wide
+// K steps into contiguous slices, as in skinny_kernel; each wave walks its
+// slice from a step rotated by workgroup (measured: without the rotation,
+// workgroups that read the same column range of their rows at once lose a
+// quarter of the bandwidth).  Per step a wave copies the tile's 16 weight
+// rows (4 instructions) and XR activation rows (XR / 4 instructions; rows
+// past M repeat row M - 1, their outputs are dropped) into one of its own S
+// LDS stages, S steps in flight, and waits for the oldest with
+// s_waitcnt vmcnt: only the wave reads its stages, so the loop has no
+// barrier.  Stage layout: rows of 256 bytes (weights, then activations),
+// 16-byte unit u of row r at slot u ^ (r & 15), so the 16 rows of a fragment
+// read fall on 16 distinct 16-byte bank groups.  Fragment j of a step is
+// MFMA j: lane group g takes k [32 j + 8 g, +8) of both operands.
+// The DMA is inline assembly (M0 operand): the compiler's own LDS DMA makes
+// it wait for every copy in flight before each LDS read.  Copies read whole
+// rows of full steps only, rows past N repeat the tile's last row, and the
+// partial last step (K % 128) goes through plain checked loads.
+template <typename T, typename TC, int XR, int S>
+__global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
+    constexpr int NQX = XR / 4, NQ = 4 + NQX;   // copies per step
+    constexpr int STG = (16 + XR) * 256;        // stage bytes
+    static_assert(XR == 4 || XR == 8 || XR == 16, "activation rows staged: 4, 8 or 16");
+    static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * S * STG];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int rows_here = min(16, (int)p.N - n0);
+
+    const int nfull = (int)(p.K / 128);
+    const int per = (nfull + 3) / 4;
+    const int c_beg = min(nfull, wave * per);
+    const int n = min(nfull, c_beg + per) - c_beg;   // wave-uniform
+
+    auto rsrc_words = [](const void* base, int64_t bytes) {
+        const uint64_t a = (uint64_t)base;
+        return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff),
+                     __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+    };
+    // ranges: the operands' read domains
+    const i32x4 rw = rsrc_words(p.W + (int64_t)n0 * p.ldb, ((int64_t)(rows_here - 1) * p.ldb + p.K) * 2);
+    const i32x4 rx = rsrc_words(p.X, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
+    int vw[4], vx[NQX];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int row = 4 * q + g;
+        vw[q] = (int)((int64_t)min(row, rows_here - 1) * p.ldb * 2) + ((l16 ^ row) << 4);
+    }
+#pragma unroll
+    for (int q = 0; q < NQX; ++q) {
+        const int t = 4 * q + g;
+        vx[q] = (int)((int64_t)min(t, (int)p.M - 1) * p.lda * 2) + ((l16 ^ t) << 4);
+    }
+    uint8_t* my = lds + wave * S * STG;
+    const int rot = n > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)n) : 0;
+    auto copy_step = [&](int i, int stage) {
+        int q = i + rot;
+        if (q >= n) q -= n;
+        const int kb = __builtin_amdgcn_readfirstlane((c_beg + q) * 256);
+        uint8_t* st = my + stage * STG;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(st + c * 1024));
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(vw[c]), "s"(rw), "s"(kb), "{m0}"(m0)
+                         : "memory");
+        }
+#pragma unroll
+        for (int c = 0; c < NQX; ++c) {
+            const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(st + 4096 + c * 1024));
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(vx[c]), "s"(rx), "s"(kb), "{m0}"(m0)
+                         : "memory");
+        }
+    };
+
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < S && i < n; ++i) copy_step(i, i);
+    int stage = 0;
+    for (int i = 0; i < n; ++i) {
+        // step i's copies are complete once at most `later` steps' remain
+        const int later = min(S - 1, n - 1 - i);
+        if (later == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NQ) : "memory");
+        else if (later == 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NQ) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * NQ) : "memory");
+        const uint8_t* st = my + stage * STG;
+        // MFMA columns t >= XR (never stored: XR >= M) repeat row t % XR
+        const int xrow = l16 & (XR - 1);
+        u32x4 wf[4], xf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int slot = ((4 * j + g) ^ l16) << 4;
+            wf[j] = *(const u32x4*)(st + l16 * 256 + slot);
+            xf[j] = *(const u32x4*)(st + 4096 + xrow * 256 + (((4 * j + g) ^ xrow) << 4));
+        }
+        // the stage is refilled only after its reads have returned
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (i + S < n) copy_step(i + S, stage);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = mfma16<T>(wf[j], xf[j], acc);
+        stage = stage + 1 == S ? 0 : stage + 1;
+    }
+
+    // partial last K step (zero-filled beyond K): the last wave, plain loads
+    if (wave == 3 && (p.K & 127)) {
+        const int kb = nfull * 128;
+        const bool xok = l16 < (int)p.M;
+        const int row = n0 + l16;
+        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+        u32x4 xt[4], wt[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int k = kb + j * 32 + g * 8;
+            const int nvalid = (int)p.K - k;
+            wt[j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
+            xt[j] = xok ? ld8_checked(p.X + (int64_t)l16 * p.lda + k, nvalid) : zero;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc = mfma16<T>(wt[j], xt[j], acc);
+    }
+
+    // the stages become the reduce buffer once every wave is done with them
+    __syncthreads();
+    float(*red)[4][64] = (float(*)[4][64])lds;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[wave][e][lane] = acc[e];
+    __syncthreads();
+
+    float alpha = p.alpha, beta = p.beta;
+    if (p.mode == 1) {
+        alpha = *(const float*)p.alpha_dev;
+        beta = *(const float*)p.beta_dev;
+    } else if (p.mode == 2) {
+        alpha = (float)*(const _Float16*)p.alpha_dev;
+        beta = (float)*(const _Float16*)p.beta_dev;
+    }
+    // output (t, o): D row o % 16 = 4 g + e, column t
+    for (int idx = tid; idx < (int)p.M * 16; idx += 256) {
+        const int t = idx >> 4, ol = idx & 15;
+        const int o = n0 + ol;
+        if (o >= (int)p.N) continue;
+        const int src_lane = (ol >> 2) * 16 + t, e = ol & 3;
+        const float s = ((red[0][e][src_lane] + red[1][e][src_lane]) + red[2][e][src_lane]) + red[3][e][src_lane];
         TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
         float y = alpha * s;
         if (beta != 0.0f) y += beta * (float)*dst;
@@ -551,6 +710,26 @@ int launch_sk(const SkParams& p, hipStream_t st) {
 
 // Shared-X decode: R weight tiles per wave (64 R rows per workgroup), MT
 // activation tiles, D K steps of weights in flight.
+// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M),
+// SKL_S steps in flight per wave.
+#ifndef VKB_SKINNY_LDS
+#define VKB_SKINNY_LDS 1
+#endif
+#ifndef SKL_S
+#define SKL_S 2
+#endif
+template <typename T, typename TC>
+int launch_sk_lds(const SkParams& p, hipStream_t st) {
+    const uint32_t grid = (p.N + 15) / 16;
+    if (p.M <= 4)
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+    else if (p.M <= 8)
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+    return (int)hipGetLastError();
+}
+
 template <typename T, typename TC, int R, int MT, int D>
 int launch_dec(const SkParams& p, float* part, int nsplit, hipStream_t st) {
     const dim3 grid((p.N + 64 * R - 1) / (64 * R), (uint32_t)nsplit);
@@ -589,6 +768,8 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
     }
     if ((int)p.M >= DEC_MIN_M)
         return f32_out ? launch_dec_mt<T, float>(p, part, nsplit, st) : launch_dec_mt<T, T>(p, part, nsplit, st);
+    if (VKB_SKINNY_LDS)
+        return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
     const bool two = p.M > 4 && (p.N + 31) / 32 >= 256;
     if (f32_out) return two ? launch_sk<T, float, 2, 4, 4>(p, st) : launch_sk<T, float, 1, 4, 4>(p, st);
     return two ? launch_sk<T, T, 2, 4, 4>(p, st) : launch_sk<T, T, 1, 4, 4>(p, st);
