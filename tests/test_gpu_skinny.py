@@ -45,6 +45,18 @@ CASES += [
     (16, 512, 520, 8, 0, 1.0, "f32"),
     (2, 4096, 4096, 0, 0, 0.0, "f32"),
 ]
+# K not a multiple of 8 (leading dimensions still are): the 8-element group
+# that straddles K must not read the NaN padding past it
+CASES += [
+    (1, 300, 1001, 7, 15, 0.0, "f16"),
+    (2, 257, 4099, 5, 13, 0.5, "bf16"),
+    (1, 64, 13, 3, 11, 0.0, "f16>f32"),
+    (3, 100, 1001, 15, 7, 0.0, "f16"),
+    (7, 129, 2051, 13, 5, 0.0, "f16>f32"),
+    (16, 64, 13, 3, 11, -0.5, "bf16"),
+    (20, 300, 1001, 7, 7, 0.0, "f16"),
+    (64, 96, 4099, 13, 5, -0.5, "bf16"),
+]
 
 
 def _padded(rows, cols, ld, seed, scale, bf=False):

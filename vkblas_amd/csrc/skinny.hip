@@ -10,23 +10,16 @@
 //
 //   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n],  m < M <= 64
 //
-// Work decomposition: a workgroup owns R tiles of 16 weight rows; its WAVES
-// waves split K into contiguous slices.  Per 128-wide K step a lane streams
-// four 16-byte pieces of one weight row and of one activation row, and feeds
-// four v_mfma_f32_16x16x32_{f16,bf16} per row tile (src A = 16 weight rows, src B =
-// up to 16 activation rows).  Lane group g = lane/16 of load / MFMA j takes k
-// in [128 c + 32 j + 8 g, +8): the same k for both operands, every k exactly
-// once, and each load instruction reads 64 contiguous bytes of each of its 16
-// rows.
-//
-// Streaming: each wave keeps D K steps of loads in flight (a rolling register
-// window; the loop is unrolled by D so window slots are static).  Loads are
-// buffer loads: the per-lane row offset is a VGPR fixed for the whole loop,
-// k goes in the scalar offset, and rows past N / activation rows past M fall
-// outside the buffer's range and read as zero.
-//
-// The waves' 16x16 partial tiles are summed in LDS in wave order (fixed
-// order: deterministic), then alpha / beta are applied once.
+// Three kernels by the number of activation rows M:
+//  * M <= 2: gemv_kernel, v_dot2 accumulation on whole-row loads;
+//  * 3 <= M <= 16: skinny_lds_kernel, one v_mfma_f32_16x16x32_{f16,bf16}
+//    tile (src A = 16 weight rows, src B = up to 16 activation rows) whose
+//    operands are copied to LDS as whole lines and read back as fragments;
+//  * 17 <= M <= 64: decode_kernel, activations shared by the workgroup's
+//    waves through LDS, K split over the grid.
+// Lane group g = lane / 16 of MFMA j takes k in [32 j + 8 g, +8) of a step:
+// the same k for both operands, every k exactly once.  Partial tiles are
+// summed in a fixed order (deterministic), then alpha / beta are applied once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "vkb_launch.h"
@@ -87,154 +80,16 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
     return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-template <typename T, typename TC, int R, int WAVES, int D>
-__global__ __launch_bounds__(WAVES * 64) void skinny_kernel(SkParams p) {
-    __shared__ float red[WAVES][R][4][64];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16 * R;
-
-    const int nsteps = (int)((p.K + 127) / 128);
-    const int full_steps = (int)(p.K / 128);
-    const int per = (nsteps + WAVES - 1) / WAVES;
-    const int c_beg = wave * per;
-    const int c_end = min(nsteps, c_beg + per);
-    const int c_full_end = max(c_beg, min(c_end, full_steps));
-
-    // buffers on this workgroup's first weight row / the activations; the
-    // record counts are the read domains ((rows - 1) ld + K elements), so
-    // rows >= N and activation rows >= M read as zero
-    const int rows_here = min(16 * R, (int)p.N - n0);
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)(((int64_t)(rows_here - 1) * p.ldb + p.K) * 2),
-        0x00020000);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + p.K) * 2), 0x00020000);
-    int w_off[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) w_off[r] = (int)(((int64_t)(r * 16 + l16) * p.ldb + g * 8) * 2);
-    const int x_off = (int)(((int64_t)l16 * p.lda + g * 8) * 2);
-
-    floatx4 acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    u32x4 wv[D][R][4], xv[D][4];
-    auto load_step = [&](int slot, int c) {
-        const int kb = c * 256;   // bytes
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) wv[slot][r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[r] + j * 64, kb, 0);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) xv[slot][j] = __builtin_amdgcn_raw_buffer_load_b128(rx, x_off + j * 64, kb, 0);
-    };
-    auto mma_step = [&](int slot) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[r] = mfma16<T>(wv[slot][r][j], xv[slot][j], acc[r]);
-    };
-
-    // full K steps [c_beg, c_full_end): rolling window of D steps.  Each
-    // workgroup walks its slice starting at a rotated step, so at any moment
-    // the workgroups read different activation lines (every workgroup uses
-    // the same activations; without the rotation they all hit the same L2
-    // lines at once).  The order is fixed per workgroup: deterministic.
-    const int nfull = c_full_end - c_beg;
-    const int rot = nfull > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)nfull) : 0;
-    auto step_of = [&](int i) {   // i-th step visited, i in [0, nfull)
-        const int q = i + rot;
-        return c_beg + (q >= nfull ? q - nfull : q);
-    };
-    int i = 0;
-    if (nfull >= D) {
-#pragma unroll
-        for (int s = 0; s < D; ++s) load_step(s, step_of(s));
-        for (; i + 2 * D <= nfull; i += D) {
-#pragma unroll
-            for (int s = 0; s < D; ++s) {
-                mma_step(s);
-                load_step(s, step_of(i + D + s));
-            }
-        }
-        // drain: the last D loaded steps, then whatever is left (< D)
-#pragma unroll
-        for (int s = 0; s < D; ++s) mma_step(s);
-        i += D;
-    }
-    for (; i < nfull; ++i) {
-        load_step(0, step_of(i));
-        mma_step(0);
-    }
-    int c = c_full_end;
-    // partial last K step (zero-filled beyond K), plain loads
-    const bool xok = l16 < (int)p.M;
-    for (; c < c_end; ++c) {
-        const int kb = c * 128;
-        u32x4 xt[4], wt[R][4];
-        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = kb + j * 32 + g * 8;
-            const int nvalid = (int)p.K - k;
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int row = n0 + r * 16 + l16;
-                wt[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
-            }
-            xt[j] = xok ? ld8_checked(p.X + (int64_t)l16 * p.lda + k, nvalid) : zero;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                acc[r] = mfma16<T>(wt[r][j], xt[j], acc[r]);
-    }
-
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[wave][r][e][lane] = acc[r][e];
-    __syncthreads();
-
-    float alpha = p.alpha, beta = p.beta;
-    if (p.mode == 1) {
-        alpha = *(const float*)p.alpha_dev;
-        beta = *(const float*)p.beta_dev;
-    } else if (p.mode == 2) {
-        alpha = (float)*(const _Float16*)p.alpha_dev;
-        beta = (float)*(const _Float16*)p.beta_dev;
-    }
-    // output (t, o): MFMA tile r = o / 16, D row = o % 16 = 4 g + e, column t
-    const int rows = 16 * R;
-    for (int idx = tid; idx < (int)p.M * rows; idx += WAVES * 64) {
-        const int t = idx / rows, ol = idx - t * rows;
-        const int o = n0 + ol;
-        if (o >= (int)p.N) continue;
-        const int r = ol >> 4, dr = ol & 15;
-        const int src_lane = (dr >> 2) * 16 + t, e = dr & 3;
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) s += red[w][r][e][src_lane];
-        TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
-        float y = alpha * s;
-        if (beta != 0.0f) y += beta * (float)*dst;
-        *dst = (TC)y;
-    }
-}
-
 // ------------------------------------------------------- staged skinny
-// For 3 <= M <= 16 activation rows, full-line loads.  skinny_kernel's loads
-// take 64 bytes of each of 16 weight rows per instruction (the MFMA fragment
-// layout); here every load is a buffer-to-LDS copy (buffer_load_dwordx4 ...
+// For 3 <= M <= 16 activation rows, full-line loads.  Loading the MFMA
+// fragment layout directly takes 64 bytes of each of 16 weight rows per
+// instruction, which measured 0.6-0.7 of HBM bandwidth; here every load is a
+// buffer-to-LDS copy (buffer_load_dwordx4 ...
 // lds: lane l writes 16 B at M0 + 16 l) of 4 rows x 256 contiguous bytes,
 // whole 128-byte lines streamed non-temporal, and the fragments are read back
 // from LDS.
 // Workgroup: one 16-row weight tile, four waves splitting the full 128-wide
-// K steps into contiguous slices, as in skinny_kernel; each wave walks its
+// K steps into contiguous slices; each wave walks its
 // slice from a step rotated by workgroup (measured: without the rotation,
 // workgroups that read the same column range of their rows at once lose a
 // quarter of the bandwidth).  Per step a wave copies the tile's 16 weight
@@ -432,16 +287,32 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
             w[r] = __builtin_amdgcn_raw_buffer_load_b128(rw, r * (int)p.ldb * 2 + kb, 0, 2);
     };
     auto compute = [&](int c, const u32x4* w, const u32x4* x) {
-        // lanes past K (last chunk) contribute nothing; the weight row's
-        // padding past K may hold anything, so both operands are zeroed
-        const bool valid = c * 512 + lane * 8 < (int)p.K;
+        // lanes past K (last chunk) contribute nothing; the padding past K
+        // may hold anything (NaN), so both operands are zeroed.  The lane
+        // whose 8 elements straddle K (K % 8 != 0) reloads them element by
+        // element, zero past K.
+        const int k = c * 512 + lane * 8;
+        const int nvalid = (int)p.K - k;
+        const bool valid = nvalid > 0;
         const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+        u32x4 ws[RB], xs[MM];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) ws[r] = w[r];
+#pragma unroll
+        for (int m = 0; m < MM; ++m) xs[m] = x[m];
+        if (valid && nvalid < 8) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+                ws[r] = r < rows_here ? ld8_checked(p.W + (int64_t)(n0 + r) * p.ldb + k, nvalid) : z;
+#pragma unroll
+            for (int m = 0; m < MM; ++m) xs[m] = ld8_checked(p.X + (int64_t)m * p.lda + k, nvalid);
+        }
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const u32x4 wr = valid ? w[r] : z;
+            const u32x4 wr = valid ? ws[r] : z;
 #pragma unroll
             for (int m = 0; m < MM; ++m) {
-                const u32x4 xm = valid ? x[m] : z;
+                const u32x4 xm = valid ? xs[m] : z;
                 float a = acc[m][r];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -519,8 +390,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
 }
 
 // ------------------------------------------------------- shared-X decode
-// For M up to 64 activation rows.  In skinny_kernel each wave reads its own
-// activation fragments, so the activations are re-read from L2 once per
+// For M up to 64 activation rows.  In skinny_lds_kernel each wave copies its
+// own activation rows, so the activations are re-read from L2 once per
 // 16-32 weight rows: at M = 64 that is 2-4x the weight bytes.  Here the four
 // waves of a workgroup own different weight rows (wave w: rows 16 R w ..
 // 16 R w + 16 R - 1 of the workgroup's 64 R) and walk the same K steps; each
@@ -701,20 +572,10 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-template <typename T, typename TC, int R, int WAVES, int D>
-int launch_sk(const SkParams& p, hipStream_t st) {
-    const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
-    hipLaunchKernelGGL((skinny_kernel<T, TC, R, WAVES, D>), dim3(grid), dim3(WAVES * 64), 0, st, p);
-    return (int)hipGetLastError();
-}
-
 // Shared-X decode: R weight tiles per wave (64 R rows per workgroup), MT
 // activation tiles, D K steps of weights in flight.
 // Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M),
 // SKL_S steps in flight per wave.
-#ifndef VKB_SKINNY_LDS
-#define VKB_SKINNY_LDS 1
-#endif
 #ifndef SKL_S
 #define SKL_S 2
 #endif
@@ -754,10 +615,8 @@ int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
 //   M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best for
 //   4096-14336 rows); more activation rows multiply its VALU work and
 //   registers.
-//   3 <= M <= DEC_MIN_M - 1: skinny_kernel: four waves split K with four
-//   steps in flight.  One 16-row tile per workgroup maximises workgroups;
-//   with more than 4 activation rows, two tiles share each activation load
-//   when that still leaves >= 256 workgroups (one per CU).
+//   3 <= M <= DEC_MIN_M - 1: skinny_lds_kernel, one 16-row tile per
+//   workgroup, four waves splitting K, two steps in flight per wave.
 //   DEC_MIN_M <= M <= 64: decode_kernel (activations shared through LDS),
 //   K split nsplit ways over the grid.
 template <typename T>
@@ -768,11 +627,7 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
     }
     if ((int)p.M >= DEC_MIN_M)
         return f32_out ? launch_dec_mt<T, float>(p, part, nsplit, st) : launch_dec_mt<T, T>(p, part, nsplit, st);
-    if (VKB_SKINNY_LDS)
-        return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
-    const bool two = p.M > 4 && (p.N + 31) / 32 >= 256;
-    if (f32_out) return two ? launch_sk<T, float, 2, 4, 4>(p, st) : launch_sk<T, float, 1, 4, 4>(p, st);
-    return two ? launch_sk<T, T, 2, 4, 4>(p, st) : launch_sk<T, T, 1, 4, 4>(p, st);
+    return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
 }
 
 }  // namespace
