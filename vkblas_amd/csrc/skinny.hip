@@ -15,8 +15,9 @@
 //  * 3 <= M <= 16: skinny_lds_kernel, one v_mfma_f32_16x16x32_{f16,bf16}
 //    tile (src A = 16 weight rows, src B = up to 16 activation rows) whose
 //    operands are copied to LDS as whole lines and read back as fragments;
-//  * 17 <= M <= 64: decode_kernel, activations shared by the workgroup's
-//    waves through LDS, K split over the grid.
+//  * 17 <= M <= 64: decode_lds_kernel, weights and activations copied to
+//    a shared LDS stage as whole lines (activations read from L2 once per
+//    128 weight rows), K split over the grid.
 // Lane group g = lane / 16 of MFMA j takes k in [32 j + 8 g, +8) of a step:
 // the same k for both operands, every k exactly once.  Partial tiles are
 // summed in a fixed order (deterministic), then alpha / beta are applied once.
@@ -55,7 +56,7 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float a) {
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x), a, false);
 }
 
-// decode_kernel from this many activation rows on; weight tiles per wave
+// decode_lds_kernel from this many activation rows on; 16-row weight tiles per wave
 constexpr int DEC_MIN_M = 17;
 constexpr int DEC_R = 2;
 
@@ -389,98 +390,86 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
     }
 }
 
-// ------------------------------------------------------- shared-X decode
-// For M up to 64 activation rows.  In skinny_lds_kernel each wave copies its
-// own activation rows, so the activations are re-read from L2 once per
-// 16-32 weight rows: at M = 64 that is 2-4x the weight bytes.  Here the four
-// waves of a workgroup own different weight rows (wave w: rows 16 R w ..
-// 16 R w + 16 R - 1 of the workgroup's 64 R) and walk the same K steps; each
-// step's activation chunk (16 MT rows x 128 k) is loaded once per workgroup
-// into LDS and read by all four waves.  The grid is filled by splitting K
+// ------------------------------------------------------- staged decode
+// For 17 <= M <= 64 activation rows.  The workgroup owns 128 weight rows
+// (wave w computes rows 32 w .. 32 w + 31, two 16-row tiles) against all
+// 16 MT activation rows (MT = ceil(M / 16) tiles), and the grid splits K
 // over blockIdx.y: with nsplit > 1 each workgroup writes raw fp32 partials
 // (part + split * M * N, row pitch N) that splitk_reduce sums in split order.
-//
-// LDS chunk layout: row r (activation row), 16-byte piece c (k 8c .. 8c+7)
-// at r * 16 + (c ^ (r & 15)) (u32x4 units).  The fragment reads (16 lanes:
-// rows r .. r+15, one piece) and the staging writes (16 threads: one row,
-// pieces 0 .. 15) then each cover all 64 banks.
-// Pipeline per K step c: load step c+D's activation chunk and then its
-// weights into a D-step register window, MFMAs of step c (activations from
-// LDS), write step c+1's chunk (loaded D-1 steps ago) to the other LDS
-// buffer, barrier.  Vector loads complete in issue order, so each wait covers
-// only the loads the step needs; everything issued later stays in flight.
-template <typename T, typename TC, int R, int MT, int D, bool PARTIAL>
-__global__ __launch_bounds__(256) void decode_kernel(SkParams p, float* part, int nsplit) {
-    __shared__ u32x4 xl[2][16 * MT * 16];
+// Per 128-wide K step the workgroup copies the 128 weight rows and the
+// activation rows into one shared LDS stage as whole 256-byte row pieces
+// (buffer_load_dwordx4 ... lds, 4 rows per instruction; wave w copies its own
+// weight rows and a quarter of the activation rows), S stages, S - 1 steps in
+// flight; each wave waits for its own copies of the oldest step with
+// s_waitcnt vmcnt, then a barrier makes the stage complete.  The activations
+// are read from L2 once per 128 weight rows.  Stage layout: rows of 256
+// bytes (weights, then activations), unit u of row r at slot u ^ (r & 15):
+// fragment reads of 16 consecutive rows are conflict-free.  Rows past N / M
+// repeat the last row (outputs dropped); the partial last K step goes through
+// plain checked loads.
+template <typename T, typename TC, int MT, int S, bool PARTIAL>
+__global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part, int nsplit) {
+    constexpr int R = DEC_R;                  // 16-row weight tiles per wave
+    constexpr int WROWS = 64 * R;             // weight rows per workgroup
+    constexpr int NQ = 4 * R + MT;            // copies per wave and step
+    constexpr int STG = (WROWS + 16 * MT) * 256;
+    static_assert(S >= 2 && S <= 4 && S * STG <= 160 * 1024 && (S - 2) * NQ < 64, "stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * STG];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
-    const int wrow0 = blockIdx.x * 64 * R + wave * 16 * R;     // this wave's first weight row
-    const int K = (int)p.K;
+    const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
+    const int wrow0 = blockIdx.x * WROWS + wave * 16 * R;     // this wave's first weight row
     const int nsteps = (K + 127) / 128, full_steps = K / 128;
     const int per = (nsteps + nsplit - 1) / nsplit;
     const int s_beg = (int)blockIdx.y * per;
-    const int n = max(0, min(nsteps, s_beg + per) - s_beg);   // uniform over the workgroup
+    const int s_end = min(nsteps, s_beg + per);
+    const int n = max(0, min(s_end, full_steps) - s_beg);      // full steps, copied
+    const bool tail = full_steps < nsteps && s_beg <= full_steps && full_steps < s_end;
 
-    // Weight buffer on this wave's first row, activation buffer on X; the
-    // record counts are the read domains, so rows past N / M read as zero.
-    const int rows_here = min(16 * R, (int)p.N - wrow0);
-    const int w_records = rows_here > 0 ? (int)(((int64_t)(rows_here - 1) * p.ldb + K) * 2) : 0;
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.W + (int64_t)max(0, min(wrow0, (int)p.N - 1)) * p.ldb), (short)0, w_records, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + K) * 2), 0x00020000);
-    int w_off[R];
+    auto rsrc_words = [](const void* base, int64_t bytes) {
+        const uint64_t a = (uint64_t)base;
+        return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                     __builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32) & 0xffff),
+                     __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+    };
+    // weight buffer on the wave's first row (clamped to the last row), range
+    // the read domain of the rows it copies
+    const int wbase = min(wrow0, N - 1);
+    const int wlast = min(wrow0 + 16 * R - 1, N - 1);
+    const i32x4 rw = rsrc_words(p.W + (int64_t)wbase * p.ldb, ((int64_t)(wlast - wbase) * p.ldb + K) * 2);
+    const i32x4 rx = rsrc_words(p.X, ((int64_t)(M - 1) * p.lda + K) * 2);
+    int vw[4 * R], vx[MT];
 #pragma unroll
-    for (int r = 0; r < R; ++r) w_off[r] = (int)(((int64_t)(r * 16 + l16) * p.ldb + g * 8) * 2);
-    // staging: thread tid moves piece tid & 15 of rows tid / 16 + 16 i
-    const int srow = tid >> 4, spc = tid & 15;
-    int x_off[MT], x_lds[MT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        const int row = srow + 16 * i;
-        x_off[i] = (int)(((int64_t)row * p.lda + spc * 8) * 2);
-        x_lds[i] = row * 16 + (spc ^ (row & 15));
+    for (int q = 0; q < 4 * R; ++q) {
+        const int rr = 4 * q + g;                               // row within the wave's 16 R
+        vw[q] = (int)((int64_t)(min(wrow0 + rr, N - 1) - wbase) * p.ldb * 2) + ((l16 ^ (rr & 15)) << 4);
     }
-    // fragment reads: row 16 t + l16, piece 4 j + g
-    int f_lds[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) f_lds[j] = l16 * 16 + ((4 * j + g) ^ l16);
-
-    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
-    auto stage_load = [&](int c, u32x4* xs) {
-        if (c < full_steps) {
+    for (int q = 0; q < MT; ++q) {
+        const int xr = wave * 4 * MT + 4 * q + g;               // activation row
+        vx[q] = (int)((int64_t)min(xr, M - 1) * p.lda * 2) + ((l16 ^ (xr & 15)) << 4);
+    }
+    // the workgroups of a K slice walk it from rotated starts, so they do
+    // not all read the same column range of their rows at once
+    const int rot = n > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)n) : 0;
+    auto copy_step = [&](int i, int stage) {
+        const int q0 = i + rot;
+        const int kb = __builtin_amdgcn_readfirstlane((s_beg + (q0 >= n ? q0 - n : q0)) * 256);
+        uint8_t* st = lds + stage * STG;
 #pragma unroll
-            for (int i = 0; i < MT; ++i) xs[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, x_off[i], c * 256, 0);
-        } else {   // partial last step: k >= K reads as zero
-#pragma unroll
-            for (int i = 0; i < MT; ++i) {
-                const int row = srow + 16 * i;
-                const int k = c * 128 + spc * 8;
-                xs[i] = row < (int)p.M ? ld8_checked(p.X + (int64_t)row * p.lda + k, K - k) : zero;
-            }
+        for (int q = 0; q < 4 * R; ++q) {
+            const int m0 = __builtin_amdgcn_readfirstlane(
+                (int)(uint32_t)(uintptr_t)(st + (wave * 16 * R + 4 * q) * 256));
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(vw[q]), "s"(rw), "s"(kb), "{m0}"(m0)
+                         : "memory");
         }
-    };
-    auto stage_store = [&](int b, const u32x4* xs) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i) xl[b][x_lds[i]] = xs[i];
-    };
-    auto w_load = [&](int c, u32x4 (*wv)[4]) {
-        if (c < full_steps) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    wv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_off[r] + j * 64, c * 256, 0);
-        } else {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = wrow0 + r * 16 + l16;
-                    const int k = c * 128 + j * 32 + g * 8;
-                    wv[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, K - k) : zero;
-                }
+        for (int q = 0; q < MT; ++q) {
+            const int m0 = __builtin_amdgcn_readfirstlane(
+                (int)(uint32_t)(uintptr_t)(st + (WROWS + wave * 4 * MT + 4 * q) * 256));
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(vx[q]), "s"(rx), "s"(kb), "{m0}"(m0)
+                         : "memory");
         }
     };
 
@@ -490,45 +479,59 @@ __global__ __launch_bounds__(256) void decode_kernel(SkParams p, float* part, in
 #pragma unroll
         for (int t = 0; t < MT; ++t) acc[r][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    u32x4 wv[D][R][4], xs[D][MT];
+    for (int i = 0; i < S - 1 && i < n; ++i) copy_step(i, i);
+    int stage = 0;
+    for (int i = 0; i < n; ++i) {
+        // this wave's copies of step i are complete once at most `later`
+        // steps' remain; the barrier then makes the whole stage complete and
+        // ends every wave's reads of the stage refilled next
+        const int later = min(S - 2, n - 1 - i);
+        if (later == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else if (later == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NQ) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * NQ) : "memory");
+        if (i + S - 1 < n) copy_step(i + S - 1, stage == 0 ? S - 1 : stage - 1);
+        const uint8_t* st = lds + stage * STG;
+        u32x4 wf[R][4], xf[MT][4];
 #pragma unroll
-    for (int s = 0; s < D; ++s)
-        if (s < n) {
-            stage_load(s_beg + s, xs[s]);
-            w_load(s_beg + s, wv[s]);
+        for (int j = 0; j < 4; ++j) {
+            const int slot = ((4 * j + g) ^ l16) << 4;
+#pragma unroll
+            for (int r = 0; r < R; ++r) wf[r][j] = *(const u32x4*)(st + (wave * 16 * R + 16 * r + l16) * 256 + slot);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) xf[t][j] = *(const u32x4*)(st + (WROWS + 16 * t + l16) * 256 + slot);
         }
-    if (n > 0) stage_store(0, xs[0]);
-    __syncthreads();
-
-    for (int i0 = 0; i0 < n; i0 += D) {
 #pragma unroll
-        for (int s = 0; s < D; ++s) {
-            const int i = i0 + s;
-            if (i < n) {                       // uniform
-                const int c = s_beg + i, b = i & 1;
-                u32x4 xf[MT][4];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int t = 0; t < MT; ++t)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) xf[t][j] = xl[b][t * 256 + f_lds[j]];
+                for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wf[r][j], xf[t][j], acc[r][t]);
+        stage = stage + 1 == S ? 0 : stage + 1;
+    }
+    if (tail) {   // partial last K step, zero-filled beyond K
+        const int kb = full_steps * 128;
+        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+        u32x4 wt[R][4], xt[MT][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j) {
+            const int k = kb + 32 * j + 8 * g;
 #pragma unroll
-                    for (int r = 0; r < R; ++r)
+            for (int r = 0; r < R; ++r) {
+                const int row = wrow0 + 16 * r + l16;
+                wt[r][j] = row < N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, K - k) : zero;
+            }
 #pragma unroll
-                        for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wv[s][r][j], xf[t][j], acc[r][t]);
-                // slot s is free again: step c+D's activations, then weights
-                if (i + D < n) {
-                    stage_load(c + D, xs[s]);
-                    w_load(c + D, wv[s]);
-                }
-                // step c+1's chunk (slot (s+1) % D) to the other buffer
-                if (i + 1 < n) stage_store(b ^ 1, xs[(s + 1) % D]);
-                // LDS traffic only: the loads in flight (registers of this
-                // wave) stay outstanding across the barrier
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            for (int t = 0; t < MT; ++t) {
+                const int xr = 16 * t + l16;
+                xt[t][j] = xr < M ? ld8_checked(p.X + (int64_t)xr * p.lda + k, K - k) : zero;
             }
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wt[r][j], xt[t][j], acc[r][t]);
     }
 
     // D row 4 g + e = weight row, column l16 = activation row: each lane
@@ -549,12 +552,12 @@ __global__ __launch_bounds__(256) void decode_kernel(SkParams p, float* part, in
         for (int t = 0; t < MT; ++t) {
             const int row = 16 * t + l16;             // activation row (output row)
             const int o = wrow0 + 16 * r + 4 * g;     // first of four weight rows (output columns)
-            if (row >= (int)p.M) continue;
+            if (row >= M) continue;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                if (o + e >= (int)p.N) continue;
+                if (o + e >= N) continue;
                 if constexpr (PARTIAL) {
-                    part[(int64_t)blockIdx.y * p.M * p.N + (int64_t)row * p.N + o + e] = acc[r][t][e];
+                    part[(int64_t)blockIdx.y * M * N + (int64_t)row * N + o + e] = acc[r][t][e];
                 } else {
                     TC* dst = (TC*)p.C + (int64_t)row * p.ldc + o + e;
                     float y = alpha * acc[r][t][e];
@@ -572,42 +575,37 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-// Shared-X decode: R weight tiles per wave (64 R rows per workgroup), MT
-// activation tiles, D K steps of weights in flight.
-// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M),
-// SKL_S steps in flight per wave.
-#ifndef SKL_S
-#define SKL_S 2
-#endif
+// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M).
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + 15) / 16;
     if (p.M <= 4)
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, 2>), dim3(grid), dim3(256), 0, st, p);
     else if (p.M <= 8)
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, 2>), dim3(grid), dim3(256), 0, st, p);
     else
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, SKL_S>), dim3(grid), dim3(256), 0, st, p);
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2>), dim3(grid), dim3(256), 0, st, p);
     return (int)hipGetLastError();
 }
 
-template <typename T, typename TC, int R, int MT, int D>
-int launch_dec(const SkParams& p, float* part, int nsplit, hipStream_t st) {
-    const dim3 grid((p.N + 64 * R - 1) / (64 * R), (uint32_t)nsplit);
+// Staged decode: MT activation tiles, three stages.
+template <typename T, typename TC, int MT>
+int launch_dec_lds(const SkParams& p, float* part, int nsplit, hipStream_t st) {
+    const dim3 grid((p.N + 64 * DEC_R - 1) / (64 * DEC_R), (uint32_t)nsplit);
     if (nsplit > 1)
-        hipLaunchKernelGGL((decode_kernel<T, float, R, MT, D, true>), grid, dim3(256), 0, st, p, part, nsplit);
+        hipLaunchKernelGGL((decode_lds_kernel<T, float, MT, 3, true>), grid, dim3(256), 0, st, p, part, nsplit);
     else
-        hipLaunchKernelGGL((decode_kernel<T, TC, R, MT, D, false>), grid, dim3(256), 0, st, p, part, nsplit);
+        hipLaunchKernelGGL((decode_lds_kernel<T, TC, MT, 3, false>), grid, dim3(256), 0, st, p, part, nsplit);
     return (int)hipGetLastError();
 }
 
 template <typename T, typename TC>
 int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
     switch ((p.M + 15) / 16) {
-        case 1: return launch_dec<T, TC, DEC_R, 1, 2>(p, part, nsplit, st);
-        case 2: return launch_dec<T, TC, DEC_R, 2, 2>(p, part, nsplit, st);
-        case 3: return launch_dec<T, TC, DEC_R, 3, 2>(p, part, nsplit, st);
-        default: return launch_dec<T, TC, DEC_R, 4, 2>(p, part, nsplit, st);
+        case 1: return launch_dec_lds<T, TC, 1>(p, part, nsplit, st);
+        case 2: return launch_dec_lds<T, TC, 2>(p, part, nsplit, st);
+        case 3: return launch_dec_lds<T, TC, 3>(p, part, nsplit, st);
+        default: return launch_dec_lds<T, TC, 4>(p, part, nsplit, st);
     }
 }
 
@@ -617,8 +615,8 @@ int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
 //   registers.
 //   3 <= M <= DEC_MIN_M - 1: skinny_lds_kernel, one 16-row tile per
 //   workgroup, four waves splitting K, two steps in flight per wave.
-//   DEC_MIN_M <= M <= 64: decode_kernel (activations shared through LDS),
-//   K split nsplit ways over the grid.
+//   DEC_MIN_M <= M <= 64: decode_lds_kernel, one workgroup per CU, K split
+//   nsplit ways over the grid.
 template <typename T>
 int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipStream_t st) {
     if (p.M <= 2) {
@@ -634,11 +632,16 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
 
 extern "C" uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K) {
     if ((int)M < DEC_MIN_M || M > 64) return 1;
-    // about two workgroups per CU, at least four K steps per slice
-    const uint32_t wg = (N + 64 * DEC_R - 1) / (64 * DEC_R);
+    const uint32_t wg = (N + 64 * DEC_R - 1) / (64 * DEC_R);   // workgroups per K slice
     const uint32_t nsteps = (K + 127) / 128;
-    uint32_t split = (512 + wg - 1) / wg;
+    // one round of workgroups (one per CU, 256 CUs): the largest split that
+    // keeps the grid within 256 workgroups, at least 4 K steps per slice.
+    // Measured on 8192x8192, 4096x14336 and 14336x4096 (17-64 tokens): a
+    // second round costs more than its shorter slices save, and slices of a
+    // few steps are dominated by filling and draining the copy pipeline.
+    uint32_t split = 256 / (wg ? wg : 1);
     if (split > nsteps / 4) split = nsteps / 4;
+    if (split > 64) split = 64;
     if (split < 1) split = 1;
     // every slice non-empty
     const uint32_t per = (nsteps + split - 1) / split;
