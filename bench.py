@@ -151,8 +151,8 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
     vdt = vk.DT_BF16 if bf16 else vk.DT_F16
     g = torch.Generator(device="cuda:0").manual_seed(11)
     Ws = [(torch.randn(O * K, device="cuda:0", generator=g) * 0.02).to(dt) for _ in range(3)]
-    X = torch.randn(16 * K, device="cuda:0", generator=g).to(dt)
-    Y = torch.empty(16 * O, device="cuda:0", dtype=dt)
+    X = torch.randn(max(ntoks) * K, device="cuda:0", generator=g).to(dt)
+    Y = torch.empty(max(ntoks) * O, device="cuda:0", dtype=dt)
     sp = stream.cuda_stream
     out = {}
     for nt in ntoks:
@@ -257,7 +257,8 @@ def main():
         print(json.dumps(fp16_gemm(torch, vk, stream, args.steps, bf16=True)))
         return
     if args.only == "matvec":
-        print(json.dumps(matvec(torch, vk, stream, args.steps)))
+        print(json.dumps({"n1-16": matvec(torch, vk, stream, args.steps),
+                          "n24-64": matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))}))
         return
     if args.only == "bf16mv":
         print(json.dumps(matvec(torch, vk, stream, args.steps, bf16=True)))
@@ -324,6 +325,8 @@ def main():
     log("[bench] decode 4096x14336 / 14336x4096")
     line["fp16_matvec_4096x14336"] = matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 16))
     line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 16))
+    log("[bench] decode 8192x8192, 24-64 tokens")
+    line["fp16_decode_8192_wide"] = matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))
     log("[bench] split-K and strided-batched")
     line["splitk_256x256"] = splitk(torch, vk, stream, args.steps, splits=(0,))
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
