@@ -131,6 +131,27 @@ def test_plan_headline_configs():
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 512, 512, 512, 512, 512, 512, batch=64).split == 1
 
 
+def test_plan_decode_split():
+    """Decode K split: up to 16 tokens none; from 17 tokens the largest split
+    that keeps the grid (128 weight rows per workgroup) within one round of
+    256 workgroups, with at least 4 K steps of 128 per slice."""
+    def split(M, N, K, ld=None):
+        ld = ld or K
+        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, M, N, K, ld, ld, N)
+        assert pl.path == vk.PATH_SKINNY
+        return pl.split
+    for M in (1, 2, 3, 16):
+        assert split(M, 8192, 8192) == 1
+    for M in (17, 24, 64):
+        assert split(M, 8192, 8192) == 4      # 64 workgroups per slice
+        assert split(M, 14336, 4096) == 2     # 112 per slice: 224 workgroups
+        assert split(M, 4096, 14336) == 8     # 32 per slice
+    assert split(32, 256, 8192) == 16         # 2 per slice, 64 steps: 4 per slice
+    assert split(32, 256, 1024) == 2          # 8 steps: at least 4 per slice
+    assert split(32, 40000, 8192) == 1        # more than one round already
+    assert split(20, 128, 100, ld=104) == 1   # a single (partial) K step
+
+
 @pytest.mark.parametrize("K", [65536, 262144])
 @pytest.mark.parametrize("split", [4, 16, 64])
 @pytest.mark.parametrize("dt", [vk.DT_F32, vk.DT_F16])
