@@ -119,20 +119,23 @@ def fp32_headline(torch, vk, stream, steps, warmup):
             "tflops_by_variant": by_variant, "launches": len(per)}
 
 
-def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False):
+def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
     """configs[2] sample: fp16 GemmEx 16F x 16F -> 16F, NN and TN (bf16: the
-    same with 16BF data and result)."""
+    same with 16BF data and result); with f32_out also 16F x 16F -> 32F."""
     dt = torch.bfloat16 if bf16 else torch.float16
     vdt = vk.DT_BF16 if bf16 else vk.DT_F16
     g = torch.Generator(device="cuda:0").manual_seed(7)
     A = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
     B = (torch.randn(n * n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
-    C = torch.empty(n * n, device="cuda:0", dtype=dt)
+    C = torch.empty(n * n, device="cuda:0", dtype=torch.float32 if f32_out else dt)
     sp = stream.cuda_stream
     out = {}
-    for name, ta in (("NN", 0), ("TN", 1)):
+    cases = [("NN", 0, vdt), ("TN", 1, vdt)]
+    if f32_out:
+        cases += [("NN_f32out", 0, vk.DT_F32), ("TN_f32out", 1, vk.DT_F32)]
+    for name, ta, cdt in cases:
         def call():
-            vk.gemm_async(vdt, vdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
+            vk.gemm_async(vdt, cdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
                           C.data_ptr(), n, stream=sp)
         for _ in range(3):
             call()
@@ -310,7 +313,7 @@ def main():
         "tflops_by_variant": h["tflops_by_variant"],
     }
     log("[bench] fp16 4096^3")
-    line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps)
+    line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps, f32_out=True)
     log("[bench] MFMA rate without memory traffic (power-limited ceiling of the 16-bit legs)")
     line["mfma_ceiling"] = mfma_ceiling(torch, vk, stream, args.steps)
     log("[bench] fp16 matvec 8192x8192")

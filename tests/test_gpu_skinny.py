@@ -57,6 +57,13 @@ CASES += [
     (20, 300, 1001, 7, 7, 0.0, "f16"),
     (64, 96, 4099, 13, 5, -0.5, "bf16"),
 ]
+# 9-16 activation rows with at least 8161 weight rows: two weight tiles per
+# workgroup (ragged last workgroup, ragged K)
+CASES += [
+    (12, 8200, 1032, 8, 8, 0.0, "f16"),
+    (16, 8192, 520, 0, 0, 0.5, "bf16"),
+    (9, 8216, 1001, 7, 15, -0.5, "f16>f32"),
+]
 
 
 def _padded(rows, cols, ld, seed, scale, bf=False):

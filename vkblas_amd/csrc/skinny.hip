@@ -89,12 +89,12 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // lds: lane l writes 16 B at M0 + 16 l) of 4 rows x 256 contiguous bytes,
 // whole 128-byte lines streamed non-temporal, and the fragments are read back
 // from LDS.
-// Workgroup: one 16-row weight tile, four waves splitting the full 128-wide
-// K steps into contiguous slices; each wave walks its
+// Workgroup: R 16-row weight tiles (R = 1 or 2), four waves splitting the
+// full 128-wide K steps into contiguous slices; each wave walks its
 // slice from a step rotated by workgroup (measured: without the rotation,
 // workgroups that read the same column range of their rows at once lose a
-// quarter of the bandwidth).  Per step a wave copies the tile's 16 weight
-// rows (4 instructions) and XR activation rows (XR / 4 instructions; rows
+// quarter of the bandwidth).  Per step a wave copies the 16 R weight rows
+// (4 R instructions) and XR activation rows (XR / 4 instructions; rows
 // past M repeat row M - 1, their outputs are dropped) into one of its own S
 // LDS stages, S steps in flight, and waits for the oldest with
 // s_waitcnt vmcnt: only the wave reads its stages, so the loop has no
@@ -106,18 +106,19 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // it wait for every copy in flight before each LDS read.  Copies read whole
 // rows of full steps only, rows past N repeat the tile's last row, and the
 // partial last step (K % 128) goes through plain checked loads.
-template <typename T, typename TC, int XR, int S>
+template <typename T, typename TC, int XR, int S, int R>
 __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
-    constexpr int NQX = XR / 4, NQ = 4 + NQX;   // copies per step
-    constexpr int STG = (16 + XR) * 256;        // stage bytes
+    constexpr int NQX = XR / 4, NQ = 4 * R + NQX;   // copies per step
+    constexpr int WR = 16 * R;                      // weight rows per workgroup
+    constexpr int STG = (WR + XR) * 256;            // stage bytes
     static_assert(XR == 4 || XR == 8 || XR == 16, "activation rows staged: 4, 8 or 16");
-    static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64, "vmcnt holds at most 63");
+    static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64 && 4 * S * STG <= 160 * 1024, "stages");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * S * STG];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
-    const int rows_here = min(16, (int)p.N - n0);
+    const int n0 = blockIdx.x * WR;
+    const int rows_here = min(WR, (int)p.N - n0);
 
     const int nfull = (int)(p.K / 128);
     const int per = (nfull + 3) / 4;
@@ -133,11 +134,11 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
     // ranges: the operands' read domains
     const i32x4 rw = rsrc_words(p.W + (int64_t)n0 * p.ldb, ((int64_t)(rows_here - 1) * p.ldb + p.K) * 2);
     const i32x4 rx = rsrc_words(p.X, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
-    int vw[4], vx[NQX];
+    int vw[4 * R], vx[NQX];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 4 * R; ++q) {
         const int row = 4 * q + g;
-        vw[q] = (int)((int64_t)min(row, rows_here - 1) * p.ldb * 2) + ((l16 ^ row) << 4);
+        vw[q] = (int)((int64_t)min(row, rows_here - 1) * p.ldb * 2) + ((l16 ^ (row & 15)) << 4);
     }
 #pragma unroll
     for (int q = 0; q < NQX; ++q) {
@@ -152,20 +153,22 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
         const int kb = __builtin_amdgcn_readfirstlane((c_beg + q) * 256);
         uint8_t* st = my + stage * STG;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < 4 * R; ++c) {
             const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(st + c * 1024));
             asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(vw[c]), "s"(rw), "s"(kb), "{m0}"(m0)
                          : "memory");
         }
 #pragma unroll
         for (int c = 0; c < NQX; ++c) {
-            const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(st + 4096 + c * 1024));
+            const int m0 = __builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(st + WR * 256 + c * 1024));
             asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(vx[c]), "s"(rx), "s"(kb), "{m0}"(m0)
                          : "memory");
         }
     };
 
-    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int i = 0; i < S && i < n; ++i) copy_step(i, i);
     int stage = 0;
     for (int i = 0; i < n; ++i) {
@@ -178,18 +181,21 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
         const uint8_t* st = my + stage * STG;
         // MFMA columns t >= XR (never stored: XR >= M) repeat row t % XR
         const int xrow = l16 & (XR - 1);
-        u32x4 wf[4], xf[4];
+        u32x4 wf[R][4], xf[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int slot = ((4 * j + g) ^ l16) << 4;
-            wf[j] = *(const u32x4*)(st + l16 * 256 + slot);
-            xf[j] = *(const u32x4*)(st + 4096 + xrow * 256 + (((4 * j + g) ^ xrow) << 4));
+#pragma unroll
+            for (int r = 0; r < R; ++r) wf[r][j] = *(const u32x4*)(st + (16 * r + l16) * 256 + slot);
+            xf[j] = *(const u32x4*)(st + WR * 256 + xrow * 256 + (((4 * j + g) ^ xrow) << 4));
         }
         // the stage is refilled only after its reads have returned
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (i + S < n) copy_step(i + S, stage);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma16<T>(wf[j], xf[j], acc);
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = mfma16<T>(wf[r][j], xf[j], acc[r]);
         stage = stage + 1 == S ? 0 : stage + 1;
     }
 
@@ -197,25 +203,32 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
     if (wave == 3 && (p.K & 127)) {
         const int kb = nfull * 128;
         const bool xok = l16 < (int)p.M;
-        const int row = n0 + l16;
         const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
-        u32x4 xt[4], wt[4];
+        u32x4 xt[4], wt[R][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int k = kb + j * 32 + g * 8;
             const int nvalid = (int)p.K - k;
-            wt[j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int row = n0 + 16 * r + l16;
+                wt[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
+            }
             xt[j] = xok ? ld8_checked(p.X + (int64_t)l16 * p.lda + k, nvalid) : zero;
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc = mfma16<T>(wt[j], xt[j], acc);
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r] = mfma16<T>(wt[r][j], xt[j], acc[r]);
     }
 
     // the stages become the reduce buffer once every wave is done with them
     __syncthreads();
-    float(*red)[4][64] = (float(*)[4][64])lds;
+    float(*red)[R][4][64] = (float(*)[R][4][64])lds;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[wave][e][lane] = acc[e];
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[wave][r][e][lane] = acc[r][e];
     __syncthreads();
 
     float alpha = p.alpha, beta = p.beta;
@@ -226,13 +239,15 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
         alpha = (float)*(const _Float16*)p.alpha_dev;
         beta = (float)*(const _Float16*)p.beta_dev;
     }
-    // output (t, o): D row o % 16 = 4 g + e, column t
-    for (int idx = tid; idx < (int)p.M * 16; idx += 256) {
-        const int t = idx >> 4, ol = idx & 15;
+    // output (t, o): tile r = o / 16, D row o % 16 = 4 g + e, column t
+    for (int idx = tid; idx < (int)p.M * WR; idx += 256) {
+        const int t = idx / WR, ol = idx - t * WR;
         const int o = n0 + ol;
         if (o >= (int)p.N) continue;
-        const int src_lane = (ol >> 2) * 16 + t, e = ol & 3;
-        const float s = ((red[0][e][src_lane] + red[1][e][src_lane]) + red[2][e][src_lane]) + red[3][e][src_lane];
+        const int r = ol >> 4, dr = ol & 15;
+        const int src_lane = (dr >> 2) * 16 + t, e = dr & 3;
+        const float s = ((red[0][r][e][src_lane] + red[1][r][e][src_lane]) + red[2][r][e][src_lane]) +
+                        red[3][r][e][src_lane];
         TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
         float y = alpha * s;
         if (beta != 0.0f) y += beta * (float)*dst;
@@ -576,15 +591,23 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
 }
 
 // Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M).
+// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering
+// M), two stages per wave.  From 9 activation rows the activation copies
+// weigh as much as the weight copies; two weight tiles per workgroup share
+// them when that still leaves one round of at least 256 workgroups
+// (measured: 8192x8192 n = 16 23.5 -> 22.3 us, K=4096, O=14336 24.0 -> 22.0
+// us; with 128 workgroups, K=14336, O=4096, 22.2 -> 29.3 us).
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
-    const uint32_t grid = (p.N + 15) / 16;
-    if (p.M <= 4)
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, 2>), dim3(grid), dim3(256), 0, st, p);
-    else if (p.M <= 8)
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, 2>), dim3(grid), dim3(256), 0, st, p);
-    else
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2>), dim3(grid), dim3(256), 0, st, p);
+    if (p.M <= 4) {
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
+    } else if (p.M <= 8) {
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
+    } else if ((p.N + 31) / 32 >= 256) {
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2, 2>), dim3((p.N + 31) / 32), dim3(256), 0, st, p);
+    } else {
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
+    }
     return (int)hipGetLastError();
 }
 
