@@ -64,6 +64,16 @@ CASES += [
     (16, 8192, 520, 0, 0, 0.5, "bf16"),
     (9, 8216, 1001, 7, 15, -0.5, "f16>f32"),
 ]
+# 17-64 activation rows on both decode geometries: R = 2 (128 weight rows per
+# workgroup, when its grid fills >= 240 CUs: K split 4, then no split with a
+# ragged last workgroup) and R = 1 (64 rows) with a ragged last workgroup;
+# the small cases above all take R = 1
+CASES += [
+    (24, 8192, 2056, 8, 8, 0.0, "f16"),
+    (40, 30720, 520, 0, 8, 0.5, "bf16"),
+    (17, 30760, 264, 8, 8, 0.0, "f16"),
+    (64, 8200, 1032, 8, 0, -0.5, "f16>f32"),
+]
 
 
 def _padded(rows, cols, ld, seed, scale, bf=False):

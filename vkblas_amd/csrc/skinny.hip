@@ -56,9 +56,39 @@ __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float a) {
         return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, w), __builtin_bit_cast(half2_t, x), a, false);
 }
 
-// decode_lds_kernel from this many activation rows on; 16-row weight tiles per wave
+// decode_lds_kernel from this many activation rows on
 constexpr int DEC_MIN_M = 17;
-constexpr int DEC_R = 2;
+
+// decode_lds_kernel geometry: R 16-row weight tiles per wave (64 R rows per
+// workgroup, R = 1 or 2) and the K split.  R = 2 (one workgroup per CU) when
+// its grid fills at least 240 of the 256 CUs in one round; otherwise R = 1,
+// whose smaller workgroups (two per CU up to 32 activation rows) spread the
+// same work over more slots.  Measured: 8192x8192 n = 17-64 R = 2 27.0-32.5
+// us against R = 1 36.4-45.8 us; K=4096, O=14336 (R = 2 fills 224 CUs) R = 2
+// 30.3-35.5 us against R = 1 24.5-34.3 us.  The split is the largest that
+// keeps the grid within one round (256 or 512 workgroups), with at least 4 K
+// steps per slice: a second round costs more than its shorter slices save,
+// and slices of a few steps are dominated by filling and draining the copy
+// pipeline.
+struct DecPlan {
+    int r;
+    uint32_t split;
+};
+__host__ __device__ inline DecPlan dec_plan(uint32_t N, uint32_t K) {
+    const uint32_t nsteps = (K + 127) / 128;
+    auto split_for = [&](uint32_t wg, uint32_t round) {
+        uint32_t sp = round / (wg ? wg : 1);
+        if (sp > nsteps / 4) sp = nsteps / 4;
+        if (sp > 64) sp = 64;
+        if (sp < 1) sp = 1;
+        const uint32_t per = (nsteps + sp - 1) / sp;   // every slice non-empty
+        return (nsteps + per - 1) / per;
+    };
+    const uint32_t wg2 = (N + 127) / 128;
+    const uint32_t s2 = split_for(wg2, 256);
+    if ((uint64_t)wg2 * s2 >= 240) return DecPlan{2, s2};
+    return DecPlan{1, split_for((N + 63) / 64, 512)};
+}
 
 struct SkParams {
     const uint16_t* X;   // 16-bit elements (fp16 or bf16 bit patterns)
@@ -406,25 +436,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
 }
 
 // ------------------------------------------------------- staged decode
-// For 17 <= M <= 64 activation rows.  The workgroup owns 128 weight rows
-// (wave w computes rows 32 w .. 32 w + 31, two 16-row tiles) against all
-// 16 MT activation rows (MT = ceil(M / 16) tiles), and the grid splits K
+// For 17 <= M <= 64 activation rows.  The workgroup owns 64 R weight rows
+// (wave w computes rows 16 R w .. 16 R w + 16 R - 1: R 16-row tiles, R = 1
+// or 2, see dec_plan) against all 16 MT activation rows (MT = ceil(M / 16)
+// tiles), and the grid splits K
 // over blockIdx.y: with nsplit > 1 each workgroup writes raw fp32 partials
 // (part + split * M * N, row pitch N) that splitk_reduce sums in split order.
-// Per 128-wide K step the workgroup copies the 128 weight rows and the
+// Per 128-wide K step the workgroup copies its weight rows and the
 // activation rows into one shared LDS stage as whole 256-byte row pieces
 // (buffer_load_dwordx4 ... lds, 4 rows per instruction; wave w copies its own
 // weight rows and a quarter of the activation rows), S stages, S - 1 steps in
 // flight; each wave waits for its own copies of the oldest step with
 // s_waitcnt vmcnt, then a barrier makes the stage complete.  The activations
-// are read from L2 once per 128 weight rows.  Stage layout: rows of 256
+// are read from L2 once per 64 R weight rows.  Stage layout: rows of 256
 // bytes (weights, then activations), unit u of row r at slot u ^ (r & 15):
 // fragment reads of 16 consecutive rows are conflict-free.  Rows past N / M
 // repeat the last row (outputs dropped); the partial last K step goes through
 // plain checked loads.
-template <typename T, typename TC, int MT, int S, bool PARTIAL>
+template <typename T, typename TC, int R, int MT, int S, bool PARTIAL>
 __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part, int nsplit) {
-    constexpr int R = DEC_R;                  // 16-row weight tiles per wave
     constexpr int WROWS = 64 * R;             // weight rows per workgroup
     constexpr int NQ = 4 * R + MT;            // copies per wave and step
     constexpr int STG = (WROWS + 16 * MT) * 256;
@@ -611,25 +641,31 @@ int launch_sk_lds(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-// Staged decode: MT activation tiles, three stages.
-template <typename T, typename TC, int MT>
+// Staged decode: R weight tiles per wave, MT activation tiles, three stages.
+template <typename T, typename TC, int R, int MT>
 int launch_dec_lds(const SkParams& p, float* part, int nsplit, hipStream_t st) {
-    const dim3 grid((p.N + 64 * DEC_R - 1) / (64 * DEC_R), (uint32_t)nsplit);
+    const dim3 grid((p.N + 64 * R - 1) / (64 * R), (uint32_t)nsplit);
     if (nsplit > 1)
-        hipLaunchKernelGGL((decode_lds_kernel<T, float, MT, 3, true>), grid, dim3(256), 0, st, p, part, nsplit);
+        hipLaunchKernelGGL((decode_lds_kernel<T, float, R, MT, 3, true>), grid, dim3(256), 0, st, p, part, nsplit);
     else
-        hipLaunchKernelGGL((decode_lds_kernel<T, TC, MT, 3, false>), grid, dim3(256), 0, st, p, part, nsplit);
+        hipLaunchKernelGGL((decode_lds_kernel<T, TC, R, MT, 3, false>), grid, dim3(256), 0, st, p, part, nsplit);
     return (int)hipGetLastError();
+}
+
+template <typename T, typename TC, int R>
+int launch_dec_r(const SkParams& p, float* part, int nsplit, hipStream_t st) {
+    switch ((p.M + 15) / 16) {
+        case 1: return launch_dec_lds<T, TC, R, 1>(p, part, nsplit, st);
+        case 2: return launch_dec_lds<T, TC, R, 2>(p, part, nsplit, st);
+        case 3: return launch_dec_lds<T, TC, R, 3>(p, part, nsplit, st);
+        default: return launch_dec_lds<T, TC, R, 4>(p, part, nsplit, st);
+    }
 }
 
 template <typename T, typename TC>
 int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
-    switch ((p.M + 15) / 16) {
-        case 1: return launch_dec_lds<T, TC, 1>(p, part, nsplit, st);
-        case 2: return launch_dec_lds<T, TC, 2>(p, part, nsplit, st);
-        case 3: return launch_dec_lds<T, TC, 3>(p, part, nsplit, st);
-        default: return launch_dec_lds<T, TC, 4>(p, part, nsplit, st);
-    }
+    return dec_plan(p.N, p.K).r == 2 ? launch_dec_r<T, TC, 2>(p, part, nsplit, st)
+                                     : launch_dec_r<T, TC, 1>(p, part, nsplit, st);
 }
 
 // One element type: output fp32 or the input type.
@@ -655,20 +691,7 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
 
 extern "C" uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K) {
     if ((int)M < DEC_MIN_M || M > 64) return 1;
-    const uint32_t wg = (N + 64 * DEC_R - 1) / (64 * DEC_R);   // workgroups per K slice
-    const uint32_t nsteps = (K + 127) / 128;
-    // one round of workgroups (one per CU, 256 CUs): the largest split that
-    // keeps the grid within 256 workgroups, at least 4 K steps per slice.
-    // Measured on 8192x8192, 4096x14336 and 14336x4096 (17-64 tokens): a
-    // second round costs more than its shorter slices save, and slices of a
-    // few steps are dominated by filling and draining the copy pipeline.
-    uint32_t split = 256 / (wg ? wg : 1);
-    if (split > nsteps / 4) split = nsteps / 4;
-    if (split > 64) split = 64;
-    if (split < 1) split = 1;
-    // every slice non-empty
-    const uint32_t per = (nsteps + split - 1) / split;
-    return (nsteps + per - 1) / per;
+    return dec_plan(N, K).split;
 }
 
 extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
