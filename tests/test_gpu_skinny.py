@@ -152,8 +152,10 @@ def test_decode_deterministic():
     import vkblas_amd as vk
     from gpu_helpers import to_dev, to_host
     print("[case] decode determinism", flush=True)
-    for M in (1, 3, 9, 40):
-        N, K = 2048, 4096
+    # every kernel and geometry: GEMV, staged skinny with one and two weight
+    # tiles per workgroup, staged decode with 64 and 128 weight rows
+    for M, N, K in ((1, 2048, 4096), (3, 2048, 4096), (9, 2048, 4096), (16, 8192, 1024), (40, 2048, 4096),
+                    (64, 8192, 2048)):
         dX, dW = to_dev(_padded(M, K, K, 21, 1.0)), to_dev(_padded(N, K, K, 22, 0.05))
         outs = []
         for _ in range(3):
