@@ -12,7 +12,7 @@ fp16 MFMA peak, 8192x8192 fp16 decode matvec vs HBM peak, with three weight
 copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched|ceiling]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched|ceiling|vendor]
 """
 import argparse
 import json
@@ -239,7 +239,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "splitk", "batched", "calibrate",
-                                       "ceiling"],
+                                       "ceiling", "vendor"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -271,6 +271,9 @@ def main():
         return
     if args.only == "batched":
         print(json.dumps(batched(torch, vk, stream, args.steps)))
+        return
+    if args.only == "vendor":
+        print(json.dumps(vendor(torch, vk, stream, args.steps)))
         return
     if args.only == "ceiling":
         print(json.dumps(mfma_ceiling(torch, vk, stream, args.steps)))
@@ -387,6 +390,37 @@ def splitk(torch, vk, stream, steps, splits=(4, 16, 64, 0)):
                     out[key]["split"] = pl.split
                     out[key]["tile"] = 64 << pl.tile
             del A, B
+    return out
+
+
+def vendor(torch, vk, stream, steps):
+    """The same workloads through PyTorch's own GEMM backend (hipBLASLt on
+    gfx950), timed like the vkblas legs: fp32 / fp16 / bf16 4096^3 (row-major
+    a @ b and a @ b.t(), i.e. hipBLAS NN and TN) and 8192x8192 fp16 decode
+    x @ w.t() with three weight copies rotated.  Not part of the default run:
+    the comparison in DESIGN.md comes from here."""
+    n = 4096
+    g = torch.Generator(device="cuda:0").manual_seed(7)
+    out = {}
+    for name, dt in (("fp32", torch.float32), ("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        a = (torch.randn(n, n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
+        b = (torch.randn(n, n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
+        bt = b.t().contiguous()
+        for lay, f in (("NN", lambda: a @ b), ("TN", lambda: a @ bt.t())):
+            for _ in range(3):
+                f()
+            med = batch_ms(torch, stream, lambda i: f(), max(steps, 20))
+            out[f"{name}_{n}_{lay}"] = {"ms": round(med, 4), "tflops": round(2.0 * n ** 3 / (med * 1e-3) / 1e12, 1)}
+    K = O = 8192
+    Ws = [(torch.randn(O, K, device="cuda:0", generator=g) * 0.02).half() for _ in range(3)]
+    X = torch.randn(64, K, device="cuda:0", generator=g).half()
+    for nt in (1, 4, 8, 16, 24, 32, 64):
+        x = X[:nt]
+        for i in range(6):
+            x @ Ws[i % 3].t()
+        med = batch_ms(torch, stream, lambda i: x @ Ws[i % 3].t(), 3 * max(steps, 10))
+        nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
+        out[f"decode_8192_n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
     return out
 
 
