@@ -124,7 +124,7 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // slice from a step rotated by workgroup (measured: without the rotation,
 // workgroups that read the same column range of their rows at once lose a
 // quarter of the bandwidth).  Per step a wave copies the 16 R weight rows
-// (4 R instructions) and XR activation rows (XR / 4 instructions; rows
+// (4 R instructions) and XR = 8 or 16 activation rows (XR / 4 instructions; rows
 // past M repeat row M - 1, their outputs are dropped) into one of its own S
 // LDS stages, S steps in flight, and waits for the oldest with
 // s_waitcnt vmcnt: only the wave reads its stages, so the loop has no
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
     constexpr int NQX = XR / 4, NQ = 4 * R + NQX;   // copies per step
     constexpr int WR = 16 * R;                      // weight rows per workgroup
     constexpr int STG = (WR + XR) * 256;            // stage bytes
-    static_assert(XR == 4 || XR == 8 || XR == 16, "activation rows staged: 4, 8 or 16");
+    static_assert(XR == 8 || XR == 16, "activation rows staged: 8 or 16");
     static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64 && 4 * S * STG <= 160 * 1024, "stages");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * S * STG];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -620,18 +620,17 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering M).
-// Staged skinny: XR activation rows staged per step (4, 8 or 16, covering
-// M), two stages per wave.  From 9 activation rows the activation copies
-// weigh as much as the weight copies; two weight tiles per workgroup share
-// them when that still leaves one round of at least 256 workgroups
-// (measured: 8192x8192 n = 16 23.5 -> 22.3 us, K=4096, O=14336 24.0 -> 22.0
-// us; with 128 workgroups, K=14336, O=4096, 22.2 -> 29.3 us).
+// Staged skinny: XR activation rows staged per step (8 or 16, covering M),
+// two stages per wave.  Up to 8 rows XR = 8 (measured against XR = 4 for
+// 3-4 rows: 8192x8192 22.0 -> 21.4 us, 4096x14336 21.6 -> 21.9 us).  From 9
+// activation rows the activation copies weigh as much as the weight copies;
+// two weight tiles per workgroup share them when that still leaves one round
+// of at least 256 workgroups (measured: 8192x8192 n = 16 23.5 -> 22.3 us,
+// K=4096, O=14336 24.0 -> 22.0 us; with 128 workgroups, K=14336, O=4096,
+// 22.2 -> 29.3 us).
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
-    if (p.M <= 4) {
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 4, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
-    } else if (p.M <= 8) {
+    if (p.M <= 8) {
         hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
     } else if ((p.N + 31) / 32 >= 256) {
         hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2, 2>), dim3((p.N + 31) / 32), dim3(256), 0, st, p);
