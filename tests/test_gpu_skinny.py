@@ -64,6 +64,13 @@ CASES += [
     (16, 8192, 520, 0, 0, 0.5, "bf16"),
     (9, 8216, 1001, 7, 15, -0.5, "f16>f32"),
 ]
+# up to 8 activation rows, at least 512 workgroups and fewer than 64 K steps:
+# two waves per workgroup (ragged K tail on the second wave; a single step)
+CASES += [
+    (5, 8200, 1032, 8, 8, 0.0, "f16"),
+    (8, 8192, 4104, 0, 8, 0.5, "bf16"),
+    (3, 8192, 136, 8, 8, -0.5, "f16>f32"),
+]
 # 17-64 activation rows on both decode geometries: R = 2 (128 weight rows per
 # workgroup, when its grid fills >= 240 CUs: K split 4, then no split with a
 # ragged last workgroup) and R = 1 (64 rows) with a ragged last workgroup;

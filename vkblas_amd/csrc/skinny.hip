@@ -119,8 +119,8 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // lds: lane l writes 16 B at M0 + 16 l) of 4 rows x 256 contiguous bytes,
 // whole 128-byte lines streamed non-temporal, and the fragments are read back
 // from LDS.
-// Workgroup: R 16-row weight tiles (R = 1 or 2), four waves splitting the
-// full 128-wide K steps into contiguous slices; each wave walks its
+// Workgroup: R 16-row weight tiles (R = 1 or 2), WAVES waves (4, or 2 for
+// short K) splitting the full 128-wide K steps into contiguous slices; each wave walks its
 // slice from a step rotated by workgroup (measured: without the rotation,
 // workgroups that read the same column range of their rows at once lose a
 // quarter of the bandwidth).  Per step a wave copies the 16 R weight rows
@@ -136,14 +136,14 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // it wait for every copy in flight before each LDS read.  Copies read whole
 // rows of full steps only, rows past N repeat the tile's last row, and the
 // partial last step (K % 128) goes through plain checked loads.
-template <typename T, typename TC, int XR, int S, int R>
-__global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
+template <typename T, typename TC, int XR, int S, int R, int WAVES = 4>
+__global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
     constexpr int NQX = XR / 4, NQ = 4 * R + NQX;   // copies per step
     constexpr int WR = 16 * R;                      // weight rows per workgroup
     constexpr int STG = (WR + XR) * 256;            // stage bytes
     static_assert(XR == 8 || XR == 16, "activation rows staged: 8 or 16");
-    static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64 && 4 * S * STG <= 160 * 1024, "stages");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[4 * S * STG];
+    static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64 && WAVES * S * STG <= 160 * 1024, "stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[WAVES * S * STG];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
     const int rows_here = min(WR, (int)p.N - n0);
 
     const int nfull = (int)(p.K / 128);
-    const int per = (nfull + 3) / 4;
+    const int per = (nfull + WAVES - 1) / WAVES;
     const int c_beg = min(nfull, wave * per);
     const int n = min(nfull, c_beg + per) - c_beg;   // wave-uniform
 
@@ -230,7 +230,7 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
     }
 
     // partial last K step (zero-filled beyond K): the last wave, plain loads
-    if (wave == 3 && (p.K & 127)) {
+    if (wave == WAVES - 1 && (p.K & 127)) {
         const int kb = nfull * 128;
         const bool xok = l16 < (int)p.M;
         const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
@@ -270,14 +270,15 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(SkParams p) {
         beta = (float)*(const _Float16*)p.beta_dev;
     }
     // output (t, o): tile r = o / 16, D row o % 16 = 4 g + e, column t
-    for (int idx = tid; idx < (int)p.M * WR; idx += 256) {
+    for (int idx = tid; idx < (int)p.M * WR; idx += 64 * WAVES) {
         const int t = idx / WR, ol = idx - t * WR;
         const int o = n0 + ol;
         if (o >= (int)p.N) continue;
         const int r = ol >> 4, dr = ol & 15;
         const int src_lane = (dr >> 2) * 16 + t, e = dr & 3;
-        const float s = ((red[0][r][e][src_lane] + red[1][r][e][src_lane]) + red[2][r][e][src_lane]) +
-                        red[3][r][e][src_lane];
+        float s = red[0][r][e][src_lane];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) s += red[w][r][e][src_lane];
         TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
         float y = alpha * s;
         if (beta != 0.0f) y += beta * (float)*dst;
@@ -628,15 +629,29 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
 // of at least 256 workgroups (measured: 8192x8192 n = 16 23.5 -> 22.3 us,
 // K=4096, O=14336 24.0 -> 22.0 us; with 128 workgroups, K=14336, O=4096,
 // 22.2 -> 29.3 us).
+template <typename T, typename TC, int XR, int R>
+void launch_skl(const SkParams& p, hipStream_t st) {
+    const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
+    // Up to 8 activation rows: two waves per workgroup (each a K half) when
+    // four would leave each wave fewer than 16 K steps and the grid has at
+    // least 512 workgroups (measured, n = 3-8: K=4096, O=14336 21.6 -> 19.5
+    // us, K=4096, O=8192 12.3-12.8 -> 11.7 us; with 16 activation rows the
+    // same split measured 0-4 % slower, so those keep four).
+    if (XR == 8 && p.K / 128 < 64 && grid >= 512) {
+        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, 2, R, 2>), dim3(grid), dim3(128), 0, st, p);
+        return;
+    }
+    hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, 2, R, 4>), dim3(grid), dim3(256), 0, st, p);
+}
+
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
-    if (p.M <= 8) {
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 8, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
-    } else if ((p.N + 31) / 32 >= 256) {
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2, 2>), dim3((p.N + 31) / 32), dim3(256), 0, st, p);
-    } else {
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, 16, 2, 1>), dim3((p.N + 15) / 16), dim3(256), 0, st, p);
-    }
+    if (p.M <= 8)
+        launch_skl<T, TC, 8, 1>(p, st);
+    else if ((p.N + 31) / 32 >= 256)
+        launch_skl<T, TC, 16, 2>(p, st);
+    else
+        launch_skl<T, TC, 16, 1>(p, st);
     return (int)hipGetLastError();
 }
 
