@@ -329,8 +329,8 @@ def main():
     line["fp16_gemm_2048"] = fp16_gemm(torch, vk, stream, args.steps, n=2048)
     line["fp16_gemm_8192"] = fp16_gemm(torch, vk, stream, args.steps, n=8192)
     log("[bench] decode 4096x14336 / 14336x4096")
-    line["fp16_matvec_4096x14336"] = matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 16))
-    line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 16))
+    line["fp16_matvec_4096x14336"] = matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 4, 8, 16))
+    line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 4, 8, 16))
     log("[bench] decode 8192x8192, 24-64 tokens")
     line["fp16_decode_8192_wide"] = matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))
     log("[bench] split-K and strided-batched")
