@@ -204,3 +204,11 @@ def test_preload_env_puts_torch_runtime_first():
     assert preload.main([]) == 2
     assert preload.torch_hipblas_command(["python3", "s.py", "-x"]) == ["python3", "-m", "vkblas_amd.torch_hipblas",
                                                                          "s.py", "-x"]
+    # interpreter options stay with the interpreter
+    assert preload.torch_hipblas_command(["python3", "-u", "-X", "dev", "s.py", "-u"]) == [
+        "python3", "-u", "-X", "dev", "-m", "vkblas_amd.torch_hipblas", "s.py", "-u"]
+    assert preload.torch_hipblas_command(["python3", "-u", "-m", "pkg.mod", "a"]) == [
+        "python3", "-u", "-m", "vkblas_amd.torch_hipblas", "-m", "pkg.mod", "a"]
+    for bad in (["python3"], ["python3", "-u"], ["python3", "-c", "print(1)"]):
+        with pytest.raises(ValueError):
+            preload.torch_hipblas_command(bad)

@@ -56,11 +56,20 @@ def preload_env(base: dict | None = None, with_torch_runtime: bool = True) -> di
     return env
 
 
+# interpreter options that take a separate argument
+_PY_OPTS_WITH_ARG = ("-W", "-X", "--check-hash-based-pycs")
+
+
 def torch_hipblas_command(argv: list) -> list:
-    """``python script.py args`` -> ``python -m vkblas_amd.torch_hipblas script.py args``."""
-    if len(argv) < 2:
-        raise ValueError("--torch-hipblas needs: <python> <script.py | -m module> [args...]")
-    return [argv[0], "-m", "vkblas_amd.torch_hipblas"] + argv[1:]
+    """``python [opts] script.py args`` -> ``python [opts] -m vkblas_amd.torch_hipblas
+    script.py args`` (``-m module`` in place of the script works the same);
+    interpreter options such as ``-u`` stay with the interpreter."""
+    i = 1
+    while i < len(argv) and argv[i].startswith("-") and argv[i] not in ("-m", "-c", "-"):
+        i += 2 if argv[i] in _PY_OPTS_WITH_ARG else 1
+    if i >= len(argv) or argv[i] in ("-c", "-"):
+        raise ValueError("--torch-hipblas needs: <python> [options] <script.py | -m module> [args...]")
+    return argv[:i] + ["-m", "vkblas_amd.torch_hipblas"] + argv[i:]
 
 
 def main(argv=None) -> int:
