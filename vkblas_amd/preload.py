@@ -84,7 +84,11 @@ def main(argv=None) -> int:
         return 2
     env = preload_env()
     if torch_hipblas:
-        argv = torch_hipblas_command(argv)
+        try:
+            argv = torch_hipblas_command(argv)
+        except ValueError as e:
+            print(e, file=sys.stderr)
+            return 2
         repo = os.path.dirname(os.path.dirname(LIB_PATH))
         env["PYTHONPATH"] = os.pathsep.join([repo] + ([env["PYTHONPATH"]] if env.get("PYTHONPATH") else []))
     return subprocess.call(argv, env=env)
