@@ -3,8 +3,8 @@
 
 Headline: fp32 GEMM M=N=K=4096, column-major,
 ld=4096, alpha=1, beta=0, all four transpose variants.  One step = the four
-variants NN, NT, TN, TT back to back through the library's C ABI (hipBLAS
-column-major call translated exactly as hipblasSgemm does).  value = total
+variants NN, NT, TN, TT back to back through the library's hipblasSgemm
+(C ABI, a hipBLAS handle on the timed stream).  value = total
 algorithmic FLOPs (2*M*N*K per GEMM) / wall time of the K timed steps.
 
 The same run also reports the other BASELINE targets (fp16 4096^3 GEMM vs the
@@ -89,11 +89,23 @@ def fp32_headline(torch, vk, stream, steps, warmup):
     B = torch.rand(n * n, device="cuda:0", generator=g) * 2 - 1
     C = torch.empty(n * n, device="cuda:0")
     sp = stream.cuda_stream
+    # through the hipBLAS entry point the north star names: hipblasSgemm on a
+    # handle whose stream is the timed stream
+    import ctypes
+    from vkblas_amd import hipblas_abi as hb
+    abi = vk.hipblas()
+    handle = abi.create()
+    if abi.hipblasSetStream(handle, sp) != hb.HIPBLAS_STATUS_SUCCESS:
+        raise RuntimeError("hipblasSetStream failed")
+    one, zero = ctypes.c_float(1.0), ctypes.c_float(0.0)
+    ops = (hb.HIPBLAS_OP_N, hb.HIPBLAS_OP_T)
+    pa, pb, pc = A.data_ptr(), B.data_ptr(), C.data_ptr()
 
     def call(ta, tb):
-        # hipBLAS (transA, transB, m, n, k) -> engine (op_a=transB, op_b=transA, M=n, N=m, A=B, B=A)
-        vk.gemm_async(vk.DT_F32, vk.DT_F32, tb, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
-                      C.data_ptr(), n, stream=sp)
+        st = abi.hipblasSgemm(handle, ops[ta], ops[tb], n, n, n, ctypes.byref(one), pa, n, pb, n, ctypes.byref(zero),
+                              pc, n)
+        if st != hb.HIPBLAS_STATUS_SUCCESS:
+            raise RuntimeError(f"hipblasSgemm failed: {st}")
 
     variants = [(0, 0), (0, 1), (1, 0), (1, 1)]
     for _ in range(warmup):
@@ -115,6 +127,7 @@ def fp32_headline(torch, vk, stream, steps, warmup):
         ts = sorted(per[i::4])
         by_variant["NT"[ta] + "NT"[tb]] = round(flops / (ts[len(ts) // 2] * 1e-3) / 1e12, 2)
     avg_ms = sum(per) / len(per)
+    abi.hipblasDestroy(handle)
     return {"wall_s": wall, "flops": flops * 4 * steps, "avg_launch_ms": avg_ms, "path": path,
             "tflops_by_variant": by_variant, "launches": len(per)}
 
@@ -178,6 +191,7 @@ def mfma_ceiling(torch, vk, stream, steps):
     on operands drawn as the 16-bit legs' data (N(0,1)/sqrt(4096)) and on
     zeros.  Under the power limit this rate depends on the data; it is the
     ceiling the 16-bit GEMM legs' frac_of_peak is held to."""
+    from vkblas_amd import bench_probe as probe
     sp = stream.cuda_stream
     blocks, iters = 256, 320                     # 172 GFLOP a launch, as long as a 4096^3 GEMM
     flops = blocks * 4 * iters * 32 * 16 * 16 * 32 * 2
@@ -191,7 +205,7 @@ def mfma_ceiling(torch, vk, stream, steps):
             ops = (ops if data == "normal" else torch.zeros_like(ops)).to(dt)
 
             def call(i):
-                vk.mfma_probe(bf16, ops.data_ptr(), out.data_ptr(), blocks, iters, stream=sp)
+                probe.mfma_probe(bf16, ops.data_ptr(), out.data_ptr(), blocks, iters, stream=sp)
             for i in range(3):
                 call(i)
             med = batch_ms(torch, stream, call, max(steps, 20))
@@ -428,8 +442,9 @@ def batched(torch, vk, stream, steps):
     """configs[4] second half: strided-batched fp32, batch 64 of 512^3 (NN)."""
     sp = stream.cuda_stream
     n, nb = 512, 64
-    A = torch.rand(nb * n * n, device="cuda:0")
-    B = torch.rand(nb * n * n, device="cuda:0")
+    g = torch.Generator(device="cuda:0").manual_seed(64)
+    A = torch.rand(nb * n * n, device="cuda:0", generator=g) * 2 - 1     # U[-1, 1), BASELINE configs[4]
+    B = torch.rand(nb * n * n, device="cuda:0", generator=g) * 2 - 1
     C = torch.empty(nb * n * n, device="cuda:0")
 
     def call():

@@ -34,6 +34,18 @@ typedef enum {
     VKBLAS_PATH_SKINNY = 5    /* bandwidth-bound skinny fp16 (M <= 16)     */
 } vkblas_path_t;
 
+/* GEMM kernel that ran (vkblas_last_kernel); the values equal the
+ * launcher's VKB_KERN_* codes. */
+typedef enum {
+    VKBLAS_KERNEL_NONE = 0,
+    VKBLAS_KERNEL_GENERIC = 1,          /* blocked MFMA kernel, whole tiles        */
+    VKBLAS_KERNEL_GENERIC_CHECKED = 2,  /* blocked MFMA kernel with edge handling  */
+    VKBLAS_KERNEL_PIPE256 = 3,          /* pipelined kernel, 256 x 256 tiles       */
+    VKBLAS_KERNEL_PIPE128 = 4,          /* pipelined kernel, 128 x 128, 2 stages   */
+    VKBLAS_KERNEL_PIPE128_4 = 5,        /* pipelined kernel, 128 x 128, 4 stages   */
+    VKBLAS_KERNEL_SKINNY = 6            /* decode kernels                          */
+} vkblas_kernel_t;
+
 typedef struct {
     int path;              /* vkblas_path_t                                 */
     int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256)  */
@@ -44,7 +56,8 @@ typedef struct {
 /*
  * General GEMM on a caller-chosen HIP stream (NULL = null stream).
  *   ab_type: type of A and B; c_type: type of C
- *     (F32, F32) | (F16, F16) | (F16, F32) | (BF16, BF16) | (BF16, F32).
+ *     (F32, F32) | (F32, F16) | (F32, BF16) | (F16, F16) | (F16, F32) |
+ *     (BF16, BF16) | (BF16, F32).
  *     fp32 accumulation throughout; 16-bit results rounded to nearest even.
  *   split_k: 0 = heuristic, 1 = never split, >1 = force that many K slices
  *            (clamped so every slice is non-empty).
@@ -65,6 +78,48 @@ vkblas_status_t vkblas_gemm_async(
     int64_t stride_a, int64_t stride_b, int64_t stride_c,
     vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
     uint32_t split_k,
+    void* stream);
+
+/*
+ * Epilogue inputs of vkblas_gemm_ex_async:
+ *   C = alpha * op(A) op(B) + beta * C_in + bias[n]
+ * computed in fp32 and rounded once to c_type.
+ *   c_in:  the matrix beta scales, of c_type, with its own leading dimension
+ *          and batch stride; NULL = C itself (the in-place BLAS form).  Read
+ *          only when beta != 0.  C_in and C must not overlap unless equal.
+ *   bias:  NULL, or N values of bias_type (F32, F16 or BF16): one per column
+ *          n of the row-major C, i.e. per row of a column-major (hipBLAS /
+ *          hipBLASLt) result, shared by every batch, added after alpha and
+ *          beta (hipBLASLt's HIPBLASLT_EPILOGUE_BIAS).
+ * No reference counterpart: the reference's engine had neither (PyTorch's
+ * addmm bias, reference test/test_torch.py:65-73, reaches the vendor
+ * library's bias epilogue on gfx950).
+ */
+typedef struct {
+    const void* c_in;
+    uint32_t ldc_in;
+    int64_t stride_c_in;
+    const void* bias;
+    vkblas_dtype_t bias_type;
+} vkblas_epilogue_t;
+
+/* vkblas_gemm_async with epilogue inputs (NULL = none: identical to
+ * vkblas_gemm_async).  Returns VKBLAS_ERR_PARAM for an unknown bias_type or
+ * ldc_in == 0 with c_in set. */
+vkblas_status_t vkblas_gemm_ex_async(
+    vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+    vkblas_op_t op_a, vkblas_op_t op_b,
+    uint32_t M, uint32_t N, uint32_t K,
+    float alpha,
+    const void* A, uint32_t lda,
+    const void* B, uint32_t ldb,
+    float beta,
+    void* C, uint32_t ldc,
+    uint32_t batch,
+    int64_t stride_a, int64_t stride_b, int64_t stride_c,
+    vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
+    uint32_t split_k,
+    const vkblas_epilogue_t* epilogue,
     void* stream);
 
 /*
@@ -111,20 +166,21 @@ vkblas_status_t vkblas_set_override(int tile, int generic);
 /* Path taken by the calling thread's most recent successful GEMM call. */
 int vkblas_last_path(void);
 
+/* Kernel (vkblas_kernel_t) the calling thread's most recent successful GEMM
+ * call launched (split-K: its pass-1 kernel). */
+int vkblas_last_kernel(void);
+
+/* Frees the split-K / decode partial buffers the library keeps per stream
+ * between calls (they are otherwise kept until the process ends, at most
+ * 4 GiB in all).  Waits for all work on every device that holds one.  Call
+ * it while no other thread is inside the library; later calls allocate
+ * again.  Returns VKBLAS_OK, or VKBLAS_ERR_INIT if a HIP call failed.  No
+ * reference counterpart (the reference's partials were grow-only,
+ * src/vkblas.c:1889-1914). */
+vkblas_status_t vkblas_workspace_release(void);
+
 /* Library version string. */
 const char* vkblas_version(void);
-
-/* MFMA rate probe (no counterpart in the reference; a measurement, not a
- * GEMM).  Launches `blocks` workgroups of four waves on `stream`; every wave
- * reads twelve 16x16x32 operand fragments once from `operands` (12 x 64
- * 16-byte units, fp16 or, with bf16 != 0, bf16 bit patterns) and issues
- * `iters` x 32 independent v_mfma_f32_16x16x32 with no memory traffic, then
- * writes one float per thread to `out` (blocks x 256 floats).  FLOPs per
- * launch: blocks x 4 x iters x 32 x 16384.  bench.py uses it to measure the
- * matrix rate the chip sustains under its power limit for given data.
- * Returns 0 or a HIP error code (bad sizes, misaligned pointers). */
-int vkblas_mfma_probe(int bf16, const void* operands, float* out, uint32_t blocks, uint32_t iters,
-                      void* stream);
 
 #ifdef __cplusplus
 }

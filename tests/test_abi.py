@@ -2,6 +2,7 @@
 symbol include/*.h declares, and its host logic (argument checks, path
 planning) behaves as documented.  No kernel is launched here."""
 import ctypes
+import importlib.util
 import os
 import re
 import subprocess
@@ -78,6 +79,23 @@ def test_no_cuda_or_oracle_dependency():
 P = vk.plan
 
 
+def test_hip_symbol_versions_within_torch_runtime():
+    """Every versioned HIP symbol the library imports is defined by the HIP
+    runtime PyTorch bundles: the library binds to that runtime inside a
+    PyTorch process (same soname), and a newer symbol version would keep it
+    from loading there."""
+    import re
+    import subprocess
+    torch_rt = os.path.join(os.path.dirname(importlib.util.find_spec("torch").origin), "lib", "libamdhip64.so")
+    if not os.path.exists(torch_rt):
+        pytest.skip("no bundled HIP runtime in this torch")
+    need = set(re.findall(r"\((hip_[0-9.]+)\)", subprocess.run(["objdump", "-T", vk.LIB_PATH], capture_output=True,
+                                                               text=True, check=True).stdout))
+    have = set(re.findall(r"\b(hip_[0-9.]+)\b", subprocess.run(["objdump", "-T", torch_rt], capture_output=True,
+                                                               text=True, check=True).stdout))
+    assert need and need <= have, sorted(need - have)
+
+
 def test_plan_rejects_bad_arguments():
     with pytest.raises(vk.VkblasError):
         P(vk.DT_F32, vk.DT_F32, 0, 0, 0, 4, 4, 4, 4, 4)          # M == 0
@@ -91,7 +109,12 @@ def test_plan_rejects_bad_arguments():
     # test/test_h.c:105 passes lda = K + M%2 < M with op_a = T)
     assert P(vk.DT_F16, vk.DT_F16, 1, 0, 8, 4, 6, 6, 4, 4).path != vk.PATH_NONE
     with pytest.raises(vk.VkblasError):
-        P(vk.DT_F32, vk.DT_F16, 0, 0, 4, 4, 4, 4, 4, 4)          # f32 in, f16 out: unsupported
+        P(vk.DT_F16, vk.DT_BF16, 0, 0, 4, 4, 4, 4, 4, 4)         # f16 in, bf16 out: unsupported
+    with pytest.raises(vk.VkblasError):
+        P(vk.DT_BF16, vk.DT_F16, 0, 0, 4, 4, 4, 4, 4, 4)         # bf16 in, f16 out: unsupported
+    # fp32 in, 16-bit out (GemmEx 32F/32F/16F and 16BF): a tile path
+    for ct in (vk.DT_F32, vk.DT_F16, vk.DT_BF16):
+        assert P(vk.DT_F32, ct, 0, 0, 4, 4, 4, 4, 4, 4).path == vk.PATH_TILE64
 
 
 def test_engine_param_errors_without_gpu():
@@ -150,6 +173,20 @@ def test_plan_decode_split():
     assert split(32, 256, 1024) == 2          # 8 steps: at least 4 per slice
     assert split(32, 40000, 8192) == 1        # more than one round already
     assert split(20, 128, 100, ld=104) == 1   # a single (partial) K step
+
+
+def test_plan_decode_span_limit():
+    """The decode kernels address a 32-row weight tile and the activation
+    rows with 32-bit buffer offsets; a decode-shaped call whose leading
+    dimensions exceed that span is planned on the tile path (which then
+    runs), never as a skinny call the launcher would refuse."""
+    big = (1 << 31) // (32 * 2)              # 32 rows of ldb fp16 elements reach 2 GiB
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 4096, 4096, 4096, big - 8, 4096).path == vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 4096, 4096, 4096, big, 4096).path != vk.PATH_SKINNY
+    # activations: 16 rows (M <= 16) or 16 ceil(M / 16) rows of lda
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, (1 << 26) - 8, 4096, 4096).path == vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, 1 << 26, 4096, 4096).path != vk.PATH_SKINNY
+    assert P(vk.DT_BF16, vk.DT_BF16, 0, 1, 17, 4096, 4096, 1 << 25, 4096, 4096).path != vk.PATH_SKINNY
 
 
 @pytest.mark.parametrize("K", [65536, 262144])

@@ -1,11 +1,11 @@
-"""vkblas_mfma_probe (the MFMA-rate measurement bench.py reports): its sums
+"""vkblas_mfma_probe (the bench-only MFMA-rate measurement bench.py reports): its sums
 are exact for constant operands, so the test checks the kernel issues every
 MFMA it claims to."""
 import pytest
 
 torch = pytest.importorskip("torch")
 
-import vkblas_amd as vk
+from vkblas_amd import bench_probe as probe
 
 pytestmark = pytest.mark.gpu
 
@@ -16,13 +16,13 @@ def test_mfma_probe_exact_sums(bf16, blocks, iters):
     dt = torch.bfloat16 if bf16 else torch.float16
     out = torch.full((blocks * 256,), float("nan"), device="cuda:0")
     ones = torch.ones(12 * 64 * 8, device="cuda:0", dtype=dt)
-    vk.mfma_probe(bf16, ones.data_ptr(), out.data_ptr(), blocks, iters)
+    probe.mfma_probe(bf16, ones.data_ptr(), out.data_ptr(), blocks, iters)
     torch.cuda.synchronize()
     # every accumulator element gains 32 (one 32-long dot product of ones) per
     # round; a thread sums 32 tiles x 4 elements
     assert torch.all(out == 32.0 * 4 * 32 * iters)
     zeros = torch.zeros_like(ones)
-    vk.mfma_probe(bf16, zeros.data_ptr(), out.data_ptr(), blocks, iters)
+    probe.mfma_probe(bf16, zeros.data_ptr(), out.data_ptr(), blocks, iters)
     torch.cuda.synchronize()
     assert torch.all(out == 0.0)
 
@@ -31,6 +31,6 @@ def test_mfma_probe_rejects_bad_arguments():
     ops = torch.zeros(12 * 64 * 8, device="cuda:0", dtype=torch.float16)
     out = torch.zeros(256, device="cuda:0")
     with pytest.raises(RuntimeError):
-        vk.mfma_probe(False, ops.data_ptr(), out.data_ptr(), 0, 1)
+        probe.mfma_probe(False, ops.data_ptr(), out.data_ptr(), 0, 1)
     with pytest.raises(RuntimeError):
-        vk.mfma_probe(False, ops.data_ptr() + 2, out.data_ptr(), 1, 1)
+        probe.mfma_probe(False, ops.data_ptr() + 2, out.data_ptr(), 1, 1)

@@ -86,8 +86,8 @@ def load():
     L.vkblas_version.restype = ctypes.c_char_p
     L.vkblas_cache_invalidate_base.argtypes = [_vp]
     L.vkblas_cache_invalidate_base.restype = None
-    L.vkblas_mfma_probe.argtypes = [_int, _vp, _vp, _u32, _u32, _vp]
-    L.vkblas_mfma_probe.restype = _int
+    L.vkblas_last_kernel.restype = _int
+    L.vkblas_workspace_release.restype = _int
     _lib = L
     return L
 
@@ -116,12 +116,21 @@ def last_path() -> int:
     return load().vkblas_last_path()
 
 
-def mfma_probe(bf16, operands, out, blocks, iters, stream=None) -> None:
-    """vkblas_mfma_probe: blocks x 4 waves x iters x 32 v_mfma_f32_16x16x32 on
-    the twelve fragments at `operands` (device pointer), no memory traffic."""
-    st = load().vkblas_mfma_probe(1 if bf16 else 0, operands, out, blocks, iters, stream)
-    if st != 0:
-        raise RuntimeError(f"vkblas_mfma_probe: HIP error {st}")
+# vkblas_kernel_t (include/vkblas_ext.h)
+KERNEL_NONE, KERNEL_GENERIC, KERNEL_GENERIC_CHECKED, KERNEL_PIPE256, KERNEL_PIPE128, KERNEL_PIPE128_4, \
+    KERNEL_SKINNY = range(7)
+
+
+def workspace_release() -> None:
+    """vkblas_workspace_release: free the per-stream partial buffers."""
+    st = load().vkblas_workspace_release()
+    if st != OK:
+        raise VkblasError(st, "vkblas_workspace_release")
+
+
+def last_kernel() -> int:
+    """vkblas_kernel_t of the calling thread's most recent successful GEMM."""
+    return load().vkblas_last_kernel()
 
 
 def gemm_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1,

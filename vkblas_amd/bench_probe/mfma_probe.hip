@@ -3,7 +3,8 @@
 // ceiling the 16-bit GEMM kernels are held to when the chip runs at its power
 // limit, which depends on the data (random fp16 mantissas toggle more
 // multiplier bits than bf16 ones, zeros hardly any).  No counterpart in the
-// reference.
+// reference, and not part of libvkblas_hipblas.so: it builds into
+// bench_probe/libvkblas_probe.so, which only bench.py and its test load.
 //
 // Each wave holds eight A and four B 16x16x32 fragments (read once from
 // `operands`: fragment f is operands[64 f + lane]) and 32 accumulator tiles,
@@ -13,7 +14,6 @@
 // loop is MFMAs and a branch only.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
-#include "vkb_launch.h"
 
 namespace {
 

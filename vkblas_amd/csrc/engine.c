@@ -16,14 +16,18 @@
  *   - launches are asynchronous on the caller's stream;
  *   - every TA/TB variant runs natively (no transposed copies, no cache).
  */
+#define _GNU_SOURCE
+#include <dlfcn.h>
 #include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 #include <hip/hip_runtime_api.h>
 
 #include "vkblas_ext.h"
 #include "vkb_launch.h"
+#include "vkb_engine.h"
 
 #define VKBLAS_VERSION_STRING "vkblas-mi355x 0.1.0 (gfx950)"
 
@@ -38,11 +42,13 @@ static int g_force_tile = -1;   /* VKBLAS_TILE = 64 | 128 | 256 */
 static uint32_t g_force_split = 0; /* VKBLAS_SPLITK = n (applies when split_k == 0) */
 static int g_no_skinny = 0;     /* VKBLAS_NO_SKINNY = 1 */
 static int g_generic_only = 0;  /* VKBLAS_KERNEL = generic */
+static int g_profile = 0;       /* VKBLAS_PROFILE */
 
 static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
 static hipMemPool_t g_pool[VKB_MAX_DEVICES];
 
 static __thread int g_last_path = VKBLAS_PATH_NONE;
+static __thread int g_last_kernel = VKBLAS_KERNEL_NONE;
 
 static void init_once(void) {
     const char* e;
@@ -57,6 +63,7 @@ static void init_once(void) {
     }
     g_no_skinny = (e = getenv("VKBLAS_NO_SKINNY")) != NULL && e[0] == '1';
     g_generic_only = (e = getenv("VKBLAS_KERNEL")) != NULL && strcmp(e, "generic") == 0;
+    g_profile = (e = getenv("VKBLAS_PROFILE")) != NULL && e[0] && e[0] != '0';
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
     g_ndev = n;
@@ -93,62 +100,179 @@ static hipMemPool_t pool_for_current_device(void) {
     return p;
 }
 
-/* Split-K partials: one workspace per (device, stream), kept between calls.
- * Work on a stream runs in order, so a call reuses its stream's workspace
- * after the kernels of the calls queued before it; calls on other streams
- * use their own.  A stream-ordered malloc / free pair per call instead left
- * the GPU idle for about 6 us between calls.  A call that needs more gets a
- * new buffer of at least twice the size (up to 1 GiB); the old one is never
- * freed, since a call on another thread may still be about to launch on it
- * (at most the last size again per stream stays allocated until exit).
- * When every slot is taken the call allocates and releases its own
- * (*owned = 1: the caller frees it on the stream after its kernels). */
+/* Split-K and decode partials (the workspace).
+ *
+ * Eager calls: one workspace per (device, stream), kept between calls.  A
+ * slot is found by the stream handle and the stream's unique id
+ * (hipStreamGetId), so a stream created at a destroyed stream's address does
+ * not inherit its buffer.  Work on a stream runs in order, so a call reuses
+ * its stream's buffer after the kernels of the calls queued before it; a
+ * stream-ordered malloc / free pair per call instead left the GPU idle for
+ * about 6 us between calls.
+ *  - A call holds its slot's lock from taking the buffer until its last
+ *    kernel is enqueued, so two threads launching on one stream cannot
+ *    interleave their pass-1 and reduce kernels on the same partials.
+ *  - A call that needs more replaces the buffer (at least twice the size, up
+ *    to 1 GiB) and frees the old one on the stream, ordered after the kernels
+ *    that used it.
+ *  - The slots hold at most VKB_WS_CACHE_BYTES together.  Calls beyond that,
+ *    calls when all slots are taken, and calls on hipStreamPerThread (one
+ *    handle value, a different stream in every thread) allocate their own
+ *    buffer and free it on the stream after their kernels.
+ * Under stream capture no buffer is handed out: a captured kernel would keep
+ * the address of a buffer that later calls reuse or free, and this library
+ * does not allocate inside a capture (graph-owned allocations are not used).
+ * Such calls fail with VKBLAS_ERR_INIT before launching anything: the hipBLAS
+ * and rocBLAS entry points then forward them to the vendor library, and
+ * engine callers use vkblas_gemm_noalloc_async, whose partials live in a
+ * fixed per-device array.  Calls that need no partials capture normally.
+ * vkblas_workspace_release() frees every cached buffer. */
 #define VKB_WS_SLOTS 64
+#define VKB_WS_CACHE_BYTES ((size_t)4 << 30)
+#define VKB_WS_GROW_CAP ((size_t)1 << 30)
 typedef struct {
+    pthread_mutex_t lock;  /* held by the call using the buffer */
     int dev;
     hipStream_t stream;
+    unsigned long long sid;
     void* ptr;
     size_t bytes;
 } ws_slot_t;
-static ws_slot_t g_ws[VKB_WS_SLOTS];
-static int g_nws = 0;
+static ws_slot_t g_ws[VKB_WS_SLOTS] = {[0 ... VKB_WS_SLOTS - 1] = {.lock = PTHREAD_MUTEX_INITIALIZER}};
+static int g_nws = 0;            /* slots claimed (never unclaimed) */
+static size_t g_ws_total = 0;    /* bytes cached in the slots */
 
-static void* stream_workspace(hipStream_t stream, size_t bytes, int* owned) {
-    *owned = 0;
+typedef struct {
+    void* ptr;
+    int slot;                    /* locked slot, or -1 */
+    int owned;                   /* free ptr on the stream after the kernels */
+    hipStream_t stream;
+} ws_lease_t;
+
+static int ws_owned(hipStream_t stream, size_t bytes, hipMemPool_t pool, ws_lease_t* L) {
+    if (hipMallocFromPoolAsync(&L->ptr, bytes, pool, stream) != hipSuccess) {
+        L->ptr = NULL;
+        return -1;
+    }
+    L->owned = 1;
+    return 0;
+}
+
+/* The stream's unique id, or 0.  hipStreamGetId is resolved at run time: HIP
+ * runtimes before 7.1 (PyTorch's bundled one among them) lack it, and a
+ * direct reference would keep the library from loading into such a
+ * process.  Without it slots are keyed by the handle value alone. */
+typedef hipError_t (*stream_id_fn_t)(hipStream_t, unsigned long long*);
+static stream_id_fn_t g_stream_id_fn;
+static pthread_once_t g_stream_id_once = PTHREAD_ONCE_INIT;
+static void stream_id_init(void) { g_stream_id_fn = (stream_id_fn_t)dlsym(RTLD_DEFAULT, "hipStreamGetId"); }
+static unsigned long long stream_id(hipStream_t stream) {
+    pthread_once(&g_stream_id_once, stream_id_init);
+    unsigned long long sid = 0;
+    if (!g_stream_id_fn || g_stream_id_fn(stream, &sid) != hipSuccess) sid = 0;
+    return sid;
+}
+
+/* 0 and L->ptr set, or -1.  Always pair with ws_release. */
+static int ws_acquire(hipStream_t stream, size_t bytes, ws_lease_t* L) {
+    L->ptr = NULL;
+    L->slot = -1;
+    L->owned = 0;
+    L->stream = stream;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return NULL;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        if (g_trace) fprintf(stderr, "[vkblas] stream is capturing: no workspace for partials, declined\n");
+        return -1;
+    }
     hipMemPool_t pool = pool_for_current_device();
-    if (!pool) return NULL;
-    void* p = NULL;
+    if (!pool) return -1;
+    if (stream == hipStreamPerThread) return ws_owned(stream, bytes, pool, L);
+    unsigned long long sid = stream_id(stream);
+
     pthread_mutex_lock(&g_pool_lock);
     int i = 0;
-    while (i < g_nws && !(g_ws[i].dev == dev && g_ws[i].stream == stream)) ++i;
-    if (i < g_nws && g_ws[i].bytes >= bytes) {
-        p = g_ws[i].ptr;
-    } else if (i < g_nws || g_nws < VKB_WS_SLOTS) {
-        size_t want = bytes;
-        if (i < g_nws) {
-            const size_t twice = g_ws[i].bytes * 2, cap = (size_t)1 << 30;
-            if (twice > want) want = twice < cap ? twice : (cap > want ? cap : want);
-        }
-        if (hipMallocFromPoolAsync(&p, want, pool, stream) != hipSuccess) {
-            p = NULL;
-        } else {
-            if (i == g_nws) {
-                g_ws[i].dev = dev;
-                g_ws[i].stream = stream;
-                ++g_nws;
-            }
-            g_ws[i].ptr = p;
-            g_ws[i].bytes = want;
-        }
-    } else if (hipMallocFromPoolAsync(&p, bytes, pool, stream) == hipSuccess) {
-        *owned = 1;
-    } else {
-        p = NULL;
+    while (i < g_nws && !(g_ws[i].dev == dev && g_ws[i].stream == stream && g_ws[i].sid == sid)) ++i;
+    if (i == g_nws && g_nws < VKB_WS_SLOTS) {
+        g_ws[i].dev = dev;
+        g_ws[i].stream = stream;
+        g_ws[i].sid = sid;
+        g_ws[i].ptr = NULL;
+        g_ws[i].bytes = 0;
+        ++g_nws;
     }
     pthread_mutex_unlock(&g_pool_lock);
-    return p;
+    if (i >= VKB_WS_SLOTS) return ws_owned(stream, bytes, pool, L);
+
+    ws_slot_t* s = &g_ws[i];
+    pthread_mutex_lock(&s->lock);
+    if (s->bytes >= bytes) {
+        L->ptr = s->ptr;
+        L->slot = i;
+        return 0;
+    }
+    size_t want = bytes;
+    if (s->bytes * 2 > want) want = s->bytes * 2 < VKB_WS_GROW_CAP ? s->bytes * 2 : (VKB_WS_GROW_CAP > want ? VKB_WS_GROW_CAP : want);
+    pthread_mutex_lock(&g_pool_lock);
+    const int fits = g_ws_total - s->bytes + want <= VKB_WS_CACHE_BYTES;
+    if (fits) g_ws_total = g_ws_total - s->bytes + want;
+    pthread_mutex_unlock(&g_pool_lock);
+    if (!fits) {
+        pthread_mutex_unlock(&s->lock);
+        return ws_owned(stream, bytes, pool, L);
+    }
+    void* p = NULL;
+    if (hipMallocFromPoolAsync(&p, want, pool, stream) != hipSuccess) {
+        pthread_mutex_lock(&g_pool_lock);
+        g_ws_total = g_ws_total + s->bytes - want;
+        pthread_mutex_unlock(&g_pool_lock);
+        pthread_mutex_unlock(&s->lock);
+        return -1;
+    }
+    if (s->ptr) hipFreeAsync(s->ptr, stream);   /* after the kernels that used it */
+    s->ptr = p;
+    s->bytes = want;
+    L->ptr = p;
+    L->slot = i;
+    return 0;
+}
+
+static void ws_release(ws_lease_t* L) {
+    if (L->owned && L->ptr) hipFreeAsync(L->ptr, L->stream);
+    if (L->slot >= 0) pthread_mutex_unlock(&g_ws[L->slot].lock);
+    L->ptr = NULL;
+    L->slot = -1;
+    L->owned = 0;
+}
+
+vkblas_status_t vkblas_workspace_release(void) {
+    pthread_once(&g_once, init_once);
+    if (g_ndev <= 0) return VKBLAS_OK;
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return VKBLAS_ERR_INIT;
+    vkblas_status_t st = VKBLAS_OK;
+    pthread_mutex_lock(&g_pool_lock);
+    for (int i = 0; i < g_nws; ++i) {
+        ws_slot_t* s = &g_ws[i];
+        pthread_mutex_lock(&s->lock);
+        if (s->ptr) {
+            /* the stream may be gone: order the free after everything on the device */
+            if (hipSetDevice(s->dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+                hipFreeAsync(s->ptr, NULL) != hipSuccess || hipStreamSynchronize(NULL) != hipSuccess)
+                st = VKBLAS_ERR_INIT;
+            g_ws_total -= s->bytes;
+            s->ptr = NULL;
+            s->bytes = 0;
+        }
+        pthread_mutex_unlock(&s->lock);
+    }
+    for (int d = 0; d < VKB_MAX_DEVICES && d < g_ndev; ++d)
+        if (g_pool[d] && (hipSetDevice(d) != hipSuccess || hipMemPoolTrimTo(g_pool[d], 0) != hipSuccess))
+            st = VKBLAS_ERR_INIT;
+    pthread_mutex_unlock(&g_pool_lock);
+    if (hipSetDevice(cur) != hipSuccess) st = VKBLAS_ERR_INIT;
+    return st;
 }
 
 /* --------------------------------------------------------------- planning */
@@ -207,7 +331,7 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (!plan) return VKBLAS_ERR_PARAM;
     memset(plan, 0, sizeof(*plan));
     if (M == 0 || N == 0 || K == 0 || batch == 0) return VKBLAS_ERR_PARAM;
-    if (!((ab_type == VKBLAS_DT_F32 && c_type == VKBLAS_DT_F32) ||
+    if (!((ab_type == VKBLAS_DT_F32 && (c_type == VKBLAS_DT_F32 || c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_BF16)) ||
           (ab_type == VKBLAS_DT_F16 && (c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_F32)) ||
           (ab_type == VKBLAS_DT_BF16 && (c_type == VKBLAS_DT_BF16 || c_type == VKBLAS_DT_F32))))
         return VKBLAS_ERR_PARAM;
@@ -217,10 +341,14 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (lda == 0 || ldb == 0 || ldc == 0) return VKBLAS_ERR_PARAM;
     if (split_k == 0 && g_force_split) split_k = g_force_split;
 
-    /* decode-shaped fp16 / bf16: X[M<=64, K] . W[N, K]^T, both K-contiguous */
+    /* decode-shaped fp16 / bf16: X[M<=64, K] . W[N, K]^T, both K-contiguous.
+     * The decode kernels address a 32-row weight tile and up to 64
+     * activation rows with 32-bit buffer offsets: larger spans take the
+     * tile path (the same bound vkb_launch_skinny enforces). */
+    const uint64_t dec_xrows = M <= 16 ? M : 16 * (((uint64_t)M + 15) / 16);
     if ((ab_type == VKBLAS_DT_F16 || ab_type == VKBLAS_DT_BF16) && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 64 &&
         batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && lda >= K && ldb >= K &&
-        !g_no_skinny) {
+        (uint64_t)32 * ldb * 2 < (1ull << 31) && dec_xrows * lda * 2 < (1ull << 31) && !g_no_skinny) {
         plan->path = VKBLAS_PATH_SKINNY;
         plan->tile = VKB_TILE_64;
         plan->split = vkb_skinny_split(M, N, K);
@@ -336,19 +464,74 @@ static const char* path_name(int p) {
     }
 }
 
-vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
-                                  vkblas_op_t op_a, vkblas_op_t op_b,
-                                  uint32_t M, uint32_t N, uint32_t K,
-                                  float alpha,
-                                  const void* A, uint32_t lda,
-                                  const void* B, uint32_t ldb,
-                                  float beta,
-                                  void* C, uint32_t ldc,
-                                  uint32_t batch,
-                                  int64_t stride_a, int64_t stride_b, int64_t stride_c,
-                                  vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
-                                  const void* beta_dev, uint32_t split_k, void* stream) {
+/* VKBLAS_PROFILE: per call, the host time to plan and enqueue and the GPU
+ * time of the call's kernels (events on the stream; the call then waits for
+ * its kernels, as every call of the reference's engine did,
+ * src/vkblas.c:954-968).  Not under stream capture. */
+typedef struct {
+    int on;
+    double t0, t1;
+    hipEvent_t e0, e1;
+} prof_t;
+
+static double now_us(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return ts.tv_sec * 1e6 + ts.tv_nsec * 1e-3;
+}
+
+static void prof_begin(prof_t* pf, hipStream_t stream) {
+    memset(pf, 0, sizeof(*pf));
+    if (!g_profile) return;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    if (hipEventCreate(&pf->e0) != hipSuccess) return;
+    if (hipEventCreate(&pf->e1) != hipSuccess) {
+        hipEventDestroy(pf->e0);
+        return;
+    }
+    pf->on = 1;
+    pf->t0 = now_us();
+    hipEventRecord(pf->e0, stream);
+}
+
+static void prof_end(prof_t* pf, hipStream_t stream, const char* what, int ok) {
+    if (!pf->on) return;
+    pf->t1 = now_us();
+    hipEventRecord(pf->e1, stream);
+    float ms = -1.0f;
+    if (ok && hipEventSynchronize(pf->e1) == hipSuccess) hipEventElapsedTime(&ms, pf->e0, pf->e1);
+    fprintf(stderr, "[vkblas] prof: %s enqueue=%.1fus gpu=%.1fus\n", what, pf->t1 - pf->t0, ms * 1e3);
+    hipEventDestroy(pf->e0);
+    hipEventDestroy(pf->e1);
+}
+
+/* The body of vkblas_gemm_async.  ws_ext != NULL: the split-K / decode
+ * partials go to that buffer of ws_ext_bytes (a call that needs more is
+ * rejected with VKBLAS_ERR_PARAM) and nothing is allocated; else the
+ * stream's workspace. */
+static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, vkblas_op_t op_a, vkblas_op_t op_b,
+                                 uint32_t M, uint32_t N, uint32_t K, float alpha, const void* A, uint32_t lda,
+                                 const void* B, uint32_t ldb, float beta, void* C, uint32_t ldc, uint32_t batch,
+                                 int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                                 vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
+                                 uint32_t split_k, const vkblas_epilogue_t* epi, void* stream, void* ws_ext,
+                                 size_t ws_ext_bytes) {
     if (!A || !B || !C) return VKBLAS_ERR_PARAM;
+    vkb_epilogue_args ep;
+    memset(&ep, 0, sizeof(ep));
+    if (epi) {
+        if (epi->bias && epi->bias_type != VKBLAS_DT_F32 && epi->bias_type != VKBLAS_DT_F16 &&
+            epi->bias_type != VKBLAS_DT_BF16)
+            return VKBLAS_ERR_PARAM;
+        if (epi->c_in && epi->ldc_in == 0) return VKBLAS_ERR_PARAM;
+        ep.c_in = epi->c_in;
+        ep.ldc_in = epi->ldc_in;
+        ep.stride_c_in = epi->stride_c_in;
+        ep.bias = epi->bias;
+        ep.bias_type = kernel_type(epi->bias_type);
+    }
+    const vkb_epilogue_args* epp = epi ? &ep : NULL;
     if (scalar_mode != VKBLAS_SCALAR_HOST && (!alpha_dev || !beta_dev)) return VKBLAS_ERR_PARAM;
     if (scalar_mode != VKBLAS_SCALAR_HOST && scalar_mode != VKBLAS_SCALAR_DEV_F32 &&
         scalar_mode != VKBLAS_SCALAR_DEV_F16)
@@ -362,26 +545,44 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
 
     const int ab = kernel_type(ab_type);
     const int ct = kernel_type(c_type);
+    const hipStream_t hs = (hipStream_t)stream;
     int rc = 0;
+    int kernel = VKBLAS_KERNEL_SKINNY;
     if (g_trace)
-        fprintf(stderr, "[vkblas] gemm %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s split=%u\n",
+        fprintf(stderr, "[vkblas] gemm %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s split=%u%s\n",
                 op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
-                path_name(plan.path), plan.split);
+                path_name(plan.path), plan.split, ws_ext ? " (scratch)" : "");
 
-    if (plan.path == VKBLAS_PATH_SKINNY && plan.split > 1) {
-        /* decode with K split over workgroups: fp32 partials, fixed-order reduce */
-        int owned = 0;
-        void* ws = stream_workspace((hipStream_t)stream, (size_t)plan.split * M * N * sizeof(float), &owned);
-        if (!ws) return VKBLAS_ERR_INIT;
+    /* partials: [split][M][N] fp32 for split-K and the split decode kernel */
+    const int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK);
+    const size_t ws_bytes = partials ? (size_t)plan.split * M * N * sizeof(float) : 0;
+    if (ws_ext && ws_bytes > ws_ext_bytes) {
+        if (g_trace)
+            fprintf(stderr, "[vkblas] partials of %zu bytes exceed the %zu-byte scratch buffer\n", ws_bytes,
+                    ws_ext_bytes);
+        return VKBLAS_ERR_PARAM;
+    }
+    prof_t pf;
+    if (!ws_ext) prof_begin(&pf, hs);
+    else memset(&pf, 0, sizeof(pf));
+    ws_lease_t lease = {NULL, -1, 0, hs};
+    void* ws = ws_ext;
+    if (partials && !ws_ext) {
+        if (ws_acquire(hs, ws_bytes, &lease) != 0) {
+            ws_release(&lease);
+            prof_end(&pf, hs, "gemm", 0);
+            return VKBLAS_ERR_INIT;
+        }
+        ws = lease.ptr;
+    }
+
+    if (plan.path == VKBLAS_PATH_SKINNY) {
+        /* decode; with a K split over workgroups: fp32 partials, fixed-order reduce */
         rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode, alpha_dev,
-                               beta_dev, (float*)ws, plan.split, stream);
-        if (rc == 0)
+                               beta_dev, epp, partials ? (float*)ws : NULL, partials ? plan.split : 1, stream);
+        if (rc == 0 && partials)
             rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
-                                          (int)scalar_mode, alpha_dev, beta_dev, stream);
-        if (owned) hipFreeAsync(ws, (hipStream_t)stream);
-    } else if (plan.path == VKBLAS_PATH_SKINNY) {
-        rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode,
-                               alpha_dev, beta_dev, NULL, 1, stream);
+                                          (int)scalar_mode, alpha_dev, beta_dev, epp, stream);
     } else {
         vkb_gemm_args a;
         memset(&a, 0, sizeof(a));
@@ -400,10 +601,9 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         a.scalar_mode = (int)scalar_mode;
         a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
         a.generic_only = g_generic_only;
+        a.kernel_out = &kernel;
+        a.epi = epp;
         if (plan.path == VKBLAS_PATH_SPLITK) {
-            int owned = 0;
-            void* ws = stream_workspace((hipStream_t)stream, (size_t)plan.split * M * N * sizeof(float), &owned);
-            if (!ws) return VKBLAS_ERR_INIT;
             a.C = ws;
             a.ldc = N;
             a.stride_c = 0;
@@ -414,21 +614,70 @@ vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             a.alpha = 1.0f; a.beta = 0.0f;
             a.scalar_mode = VKB_SCALAR_HOST;
             a.alpha_dev = a.beta_dev = NULL;
+            a.epi = NULL;
             rc = vkb_launch_gemm(&a, plan.tile, stream);
             if (rc == 0)
                 rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct,
-                                              alpha, beta, (int)scalar_mode, alpha_dev, beta_dev, stream);
-            if (owned) hipFreeAsync(ws, (hipStream_t)stream);
+                                              alpha, beta, (int)scalar_mode, alpha_dev, beta_dev, epp, stream);
         } else {
             rc = vkb_launch_gemm(&a, plan.tile, stream);
         }
     }
+    ws_release(&lease);
+    prof_end(&pf, hs, path_name(plan.path), rc == 0);
     if (rc != 0) {
         if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s\n", hipGetErrorString((hipError_t)rc));
         return VKBLAS_ERR_INIT;
     }
     g_last_path = plan.path;
+    g_last_kernel = kernel;
     return VKBLAS_OK;
+}
+
+vkblas_status_t vkblas_gemm_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+                                  vkblas_op_t op_a, vkblas_op_t op_b,
+                                  uint32_t M, uint32_t N, uint32_t K,
+                                  float alpha,
+                                  const void* A, uint32_t lda,
+                                  const void* B, uint32_t ldb,
+                                  float beta,
+                                  void* C, uint32_t ldc,
+                                  uint32_t batch,
+                                  int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                                  vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
+                                  const void* beta_dev, uint32_t split_k, void* stream) {
+    return gemm_impl(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, stride_a,
+                     stride_b, stride_c, scalar_mode, alpha_dev, beta_dev, split_k, NULL, stream, NULL, 0);
+}
+
+vkblas_status_t vkblas_gemm_ex_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+                                     vkblas_op_t op_a, vkblas_op_t op_b,
+                                     uint32_t M, uint32_t N, uint32_t K,
+                                     float alpha,
+                                     const void* A, uint32_t lda,
+                                     const void* B, uint32_t ldb,
+                                     float beta,
+                                     void* C, uint32_t ldc,
+                                     uint32_t batch,
+                                     int64_t stride_a, int64_t stride_b, int64_t stride_c,
+                                     vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
+                                     const void* beta_dev, uint32_t split_k,
+                                     const vkblas_epilogue_t* epilogue, void* stream) {
+    return gemm_impl(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, stride_a,
+                     stride_b, stride_c, scalar_mode, alpha_dev, beta_dev, split_k, epilogue, stream, NULL, 0);
+}
+
+vkblas_status_t vkb_gemm_with_scratch(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, vkblas_op_t op_a,
+                                      vkblas_op_t op_b, uint32_t M, uint32_t N, uint32_t K, float alpha,
+                                      const void* A, uint32_t lda, const void* B, uint32_t ldb, float beta,
+                                      void* C, uint32_t ldc, uint32_t batch, int64_t stride_a, int64_t stride_b,
+                                      int64_t stride_c, vkblas_scalar_mode_t scalar_mode, const void* alpha_dev,
+                                      const void* beta_dev, uint32_t split_k, void* stream, void* scratch,
+                                      size_t scratch_bytes) {
+    if (!scratch || scratch_bytes == 0) return VKBLAS_ERR_PARAM;
+    return gemm_impl(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch, stride_a,
+                     stride_b, stride_c, scalar_mode, alpha_dev, beta_dev, split_k, NULL, stream, scratch,
+                     scratch_bytes);
 }
 
 vkblas_status_t vkblas_gemm_batched_async(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
@@ -475,16 +724,24 @@ vkblas_status_t vkblas_gemm_batched_async(vkblas_dtype_t ab_type, vkblas_dtype_t
     a.scalar_mode = (int)scalar_mode;
     a.alpha_dev = alpha_dev; a.beta_dev = beta_dev;
     a.ptr_array = 1;
+    int kernel = VKBLAS_KERNEL_NONE;
+    a.kernel_out = &kernel;
+    prof_t pf;
+    prof_begin(&pf, (hipStream_t)stream);
     const int rc = vkb_launch_gemm(&a, plan.tile, stream);
+    prof_end(&pf, (hipStream_t)stream, "batched", rc == 0);
     if (rc != 0) {
         if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s\n", hipGetErrorString((hipError_t)rc));
         return VKBLAS_ERR_INIT;
     }
     g_last_path = plan.path;
+    g_last_kernel = kernel;
     return VKBLAS_OK;
 }
 
 int vkblas_last_path(void) { return g_last_path; }
+
+int vkblas_last_kernel(void) { return g_last_kernel; }
 
 vkblas_status_t vkblas_set_override(int tile, int generic) {
     pthread_once(&g_once, init_once);

@@ -73,6 +73,14 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     p.alpha = a->alpha; p.beta = a->beta;
     p.scalar_mode = a->scalar_mode;
     p.alpha_dev = a->alpha_dev; p.beta_dev = a->beta_dev;
+    const vkb_epilogue_args* ep = a->epi;
+    const bool sep_cin = ep && ep->c_in && p.split == 1;   // pass 1 writes raw partials
+    p.epi.cin = sep_cin ? ep->c_in : a->C;
+    p.epi.ldcin = sep_cin ? ep->ldc_in : a->ldc;
+    p.epi.scin = sep_cin ? ep->stride_c_in : a->stride_c;
+    p.epi.bias = (ep && p.split == 1) ? ep->bias : nullptr;
+    p.epi.bias_type = ep ? ep->bias_type : 0;
+    if (p.ptr_array && sep_cin) return (int)hipErrorInvalidValue;   // Cin pointers are not given
     const bool multi = p.batch > 1;
     p.ptr_array = a->ptr_array != 0;
     if (p.ptr_array) {
@@ -87,7 +95,18 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
         p.vec_b = (a->ldb % VEC == 0) && aligned(a->B, 16) && (!multi || a->stride_b % VEC == 0);
         p.vec_c = (a->ldc % 4 == 0) && aligned(a->C, 4 * sizeof(TC)) && (!multi || a->stride_c % 4 == 0) &&
                   (p.split == 1 || p.s_split % 4 == 0);
+        if (sep_cin)   // Cin is read with the same vector width as C
+            p.vec_c = p.vec_c && p.epi.ldcin % 4 == 0 && aligned(p.epi.cin, 4 * sizeof(TC)) &&
+                      (!multi || p.epi.scin % 4 == 0);
     }
+    {
+        constexpr int64_t CV = 16 / sizeof(TC);   // elements per 16 bytes of C
+        p.c_rows16 = !p.ptr_array && a->ldc % CV == 0 && aligned(a->C, 16) && (!multi || a->stride_c % CV == 0) &&
+                     (p.split == 1 || p.s_split % CV == 0);
+    }
+    auto report = [&](int k) {
+        if (a->kernel_out) *a->kernel_out = k;
+    };
     if (p.split > 1 && (p.kps == 0 || p.kps % BK != 0)) return (int)hipErrorInvalidValue;
 
     const bool full = !p.ptr_array && (a->M % bm == 0) && (a->N % bn == 0) && (a->K % BK == 0) &&
@@ -109,6 +128,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
         const bool pipe_ok = full && (p.split == 1 || p.kps % KPAIR == 0) && !a->generic_only &&
                              a->K % KPAIR == 0 && span_a < (1ull << 31) && span_b < (1ull << 31);
         if (tile == VKB_TILE_256 && pipe_ok) {
+            report(VKB_KERN_PIPE256);
             if (ak) {
                 if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true>), dim3(grid), dim3(256), 0, st, p);
                 else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false>), dim3(grid), dim3(256), 0, st, p);
@@ -123,6 +143,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             // four LDS stages when the grid is at most one workgroup per CU
             // (the 144 KB they take allow no second one), else two
             if (tile == VKB_TILE_128 && pipe_ok) {
+                report(grid <= cu_count() ? VKB_KERN_PIPE128_4 : VKB_KERN_PIPE128);
                 if (grid <= cu_count()) {
                     if (ak) {
                         if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64, 4>), dim3(grid), dim3(256), 0, st, p);
@@ -142,6 +163,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             }
         }
     }
+    report(full ? VKB_KERN_GENERIC : VKB_KERN_GENERIC_CHECKED);
     switch (tile) {
         case VKB_TILE_64:  return launch_layout<T, TC, VKB_TILE_64>(p, ak, bk, !full, grid, st);
         case VKB_TILE_128: return launch_layout<T, TC, VKB_TILE_128>(p, ak, bk, !full, grid, st);

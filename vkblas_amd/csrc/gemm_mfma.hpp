@@ -29,6 +29,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "epilogue.hpp"
 
 namespace vkb {
 
@@ -56,6 +57,12 @@ struct KParams {
     const void* beta_dev;
     int scalar_mode;
     int vec_a, vec_b, vec_c;
+    // every C row starts 16-byte aligned (ldc * sizeof(TC) % 16 == 0, C, the
+    // batch stride and the split-K stride too): the pipelined kernel's
+    // staged epilogue stores whole rows in 16-byte units
+    int c_rows16;
+    // Cin (beta's matrix) and the bias vector; vec_c covers Cin's alignment too
+    EpiParams epi;
     // A, B, C are device arrays of `batch` matrix pointers (the sa / sb / sc
     // strides are unused); vec_* then also need each matrix aligned, which
     // the kernel checks per batch
@@ -313,11 +320,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
     const T* Ab;
     const T* Bb;
     TC* Cb;
+    const TC* Ci;   // beta's matrix (Cb itself in place)
     bool va = p.vec_a != 0, vb = p.vec_b != 0, vc = p.vec_c != 0;
     if (p.ptr_array) {
         Ab = ((const T* const*)p.A)[b];
         Bb = ((const T* const*)p.B)[b];
         Cb = ((TC* const*)p.C)[b];
+        Ci = Cb;
         va = va && ((uintptr_t)Ab & 15) == 0;
         vb = vb && ((uintptr_t)Bb & 15) == 0;
         vc = vc && ((uintptr_t)Cb & (4 * sizeof(TC) - 1)) == 0;
@@ -325,7 +334,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
         Ab = (const T*)p.A + (int64_t)b * p.sa;
         Bb = (const T*)p.B + (int64_t)b * p.sb;
         Cb = (TC*)p.C + (int64_t)b * p.sc + (int64_t)s * p.s_split;
+        Ci = (const TC*)p.epi.cin + (int64_t)b * p.epi.scin;
     }
+    const int64_t ldci = p.ptr_array ? p.ldc : p.epi.ldcin;
     const int kbeg = (int)(s * p.kps);
     const int kend = (int)min((uint32_t)p.K, s * p.kps + p.kps);
     const int nkt = (kend - kbeg + BK - 1) / BK;
@@ -428,6 +439,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
         const int m = m0 + wm * WTM + i * 32 + l32;
         if (CHECKED && m >= (int)p.M) continue;
         TC* crow = Cb + (int64_t)m * p.ldc;
+        const TC* cirow = Ci + (int64_t)m * ldci;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
 #pragma unroll
@@ -439,30 +451,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(KParams p) {
                 if constexpr (!CHECKED) {
                     if (beta != 0.0f) {
                         float o[4];
-                        load4<TC>(crow + n, o, true);
+                        load4<TC>(cirow + n, o, true);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) x[e] += beta * o[e];
                     }
+                    add_bias4(p.epi, n, 4, x);
                     store4<TC>(crow + n, x, true);
                 } else {
                     const int nv = (int)p.N - n;
                     if (nv >= 4) {
                         if (beta != 0.0f) {
                             float o[4];
-                            load4<TC>(crow + n, o, vc);
+                            load4<TC>(cirow + n, o, vc);
 #pragma unroll
                             for (int e = 0; e < 4; ++e) x[e] += beta * o[e];
                         }
+                        add_bias4(p.epi, n, 4, x);
                         store4<TC>(crow + n, x, vc);
                     } else {
+                        if (beta != 0.0f) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (e < nv) {
-                                float y = x[e];
-                                if (beta != 0.0f) y += beta * (float)crow[n + e];
-                                crow[n + e] = (TC)y;
-                            }
+                            for (int e = 0; e < 4; ++e)
+                                if (e < nv) x[e] += beta * (float)cirow[n + e];
                         }
+                        add_bias4(p.epi, n, nv, x);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (e < nv) crow[n + e] = (TC)x[e];
                     }
                 }
             }

@@ -554,7 +554,26 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     load_scalars(p, alpha, beta);
     constexpr int NQ = SH == 0 ? 1 : 4;
     const float beta_u = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, beta)));
-    if (beta_u == 0.0f) {
+    // bias of this lane's output columns, loaded once (inside the unrolled
+    // store loops the per-element loads make them too large to unroll)
+    const bool has_bias = p.epi.bias != nullptr;
+    float bcol[NF][NQ][4];
+#pragma unroll
+    for (int j = 0; j < NF; ++j)
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bcol[j][q][e] = 0.0f;
+    if (has_bias) {
+        const int nb = n0 + wn * WT + (SH == 0 ? 4 * (lane >> 4) : h * 4);
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bcol[j][q][e] = bias_at(p.epi, nb + j * FR + q * 8 + e);
+    }
+    if (beta_u == 0.0f && p.c_rows16) {
         // Staged through LDS so C leaves as whole rows: the MFMA layout
         // spreads a store instruction over 16-32 rows of C, the texture
         // address unit then handles a line per row.  The rows are stored
@@ -587,6 +606,10 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
                         float x[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e];
+                        if (has_bias) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) x[e] += bcol[j][q][e];
+                        }
                         store4<TC>((TC*)(wl + m * STR + n * (int)sizeof(TC)), x, true);
                     }
                 }
@@ -603,19 +626,32 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
     } else {
+        // Direct stores of 4 consecutive n per lane (16 B fp32, 8 B 16-bit:
+        // the launcher's vec_c alignment); C is read only when beta != 0, so
+        // a NaN in C never reaches a beta == 0 result.  Rows that are not
+        // 16-byte aligned (16-bit C with ldc % 8 == 4, or C at an 8-byte
+        // offset) take this path with beta == 0 as well.
+        const bool rd = beta_u != 0.0f;
+        const TC* Ci = (const TC*)p.epi.cin + (sk ? 0 : (int64_t)b * p.epi.scin);
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int m = m0 + wm * WT + i * FR + fl;
             TC* crow = Cb + (int64_t)m * p.ldc;
+            const TC* cirow = Ci + (int64_t)m * p.epi.ldcin;
 #pragma unroll
             for (int j = 0; j < NF; ++j) {
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
                     const int n = n0 + wn * WT + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
-                    float x[4], o[4];
-                    load4<TC>(crow + n, o, true);
+                    float x[4], o[4] = {0.f, 0.f, 0.f, 0.f};
+                    if (rd) load4<TC>(cirow + n, o, true);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) x[e] = alpha * acc[i][j][q * 4 + e] + beta * o[e];
+                    for (int e = 0; e < 4; ++e) x[e] = rd ? alpha * acc[i][j][q * 4 + e] + beta * o[e]
+                                                          : alpha * acc[i][j][q * 4 + e];
+                    if (has_bias) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) x[e] += bcol[j][q][e];
+                    }
                     store4<TC>(crow + n, x, true);
                 }
             }

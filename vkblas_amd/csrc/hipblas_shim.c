@@ -302,8 +302,11 @@ static int compute_kind(int c) {
 static int ex_types(int at, int bt, int ctp, int comp, vkblas_dtype_t* ab, vkblas_dtype_t* ct, int* scal_f16) {
     const int kind = compute_kind(comp);
     if (kind == 0) return 0;
-    if (is_f32_t(at) && is_f32_t(bt) && is_f32_t(ctp) && kind == 1) {
-        *ab = VKBLAS_DT_F32; *ct = VKBLAS_DT_F32; *scal_f16 = 0;
+    if (is_f32_t(at) && is_f32_t(bt) && kind == 1 && (is_f32_t(ctp) || is_f16_t(ctp) || is_bf16_t(ctp))) {
+        /* fp32 in, fp32 / fp16 / bf16 out (the 16-bit results rounded once) */
+        *ab = VKBLAS_DT_F32;
+        *ct = is_f32_t(ctp) ? VKBLAS_DT_F32 : is_f16_t(ctp) ? VKBLAS_DT_F16 : VKBLAS_DT_BF16;
+        *scal_f16 = 0;
         return 1;
     }
     if (is_f16_t(at) && is_f16_t(bt) && (is_f16_t(ctp) || is_f32_t(ctp))) {

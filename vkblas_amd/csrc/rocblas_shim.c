@@ -156,7 +156,6 @@ static int run(const gemm_call* g) {
     vkblas_dtype_t ab, cb, ct, dt;
     if (!dtype_of(g->a_type, &ab) || !dtype_of(g->b_type, &cb) || ab != cb) return 1;
     if (!dtype_of(g->c_type, &ct) || !dtype_of(g->d_type, &dt) || ct != dt) return 1;
-    if (ab == VKBLAS_DT_F32 && ct != VKBLAS_DT_F32) return 1;
 
     hipStream_t stream = NULL;
     rocblas_pointer_mode mode = rocblas_pointer_mode_host;

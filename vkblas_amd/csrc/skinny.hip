@@ -23,6 +23,7 @@
 // summed in a fixed order (deterministic), then alpha / beta are applied once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "epilogue.hpp"
 #include "vkb_launch.h"
 
 namespace {
@@ -100,6 +101,7 @@ struct SkParams {
     int mode;
     const void* alpha_dev;
     const void* beta_dev;
+    vkb::EpiParams epi;   // Cin (beta's matrix) and bias per output column o
 };
 
 __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
@@ -281,7 +283,8 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
         for (int w = 1; w < WAVES; ++w) s += red[w][r][e][src_lane];
         TC* dst = (TC*)p.C + (int64_t)t * p.ldc + o;
         float y = alpha * s;
-        if (beta != 0.0f) y += beta * (float)*dst;
+        if (beta != 0.0f) y += beta * (float)((const TC*)p.epi.cin)[(int64_t)t * p.epi.ldcin + o];
+        if (p.epi.bias) y += vkb::bias_at(p.epi, o);
         *dst = (TC)y;
     }
 }
@@ -430,7 +433,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
             const float s = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
             TC* dst = (TC*)p.C + (int64_t)m * p.ldc + n0 + r;
             float y = alpha * s;
-            if (beta != 0.0f) y += beta * (float)*dst;
+            if (beta != 0.0f) y += beta * (float)((const TC*)p.epi.cin)[(int64_t)m * p.epi.ldcin + n0 + r];
+            if (p.epi.bias) y += vkb::bias_at(p.epi, n0 + r);
             *dst = (TC)y;
         }
     }
@@ -607,7 +611,8 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
                 } else {
                     TC* dst = (TC*)p.C + (int64_t)row * p.ldc + o + e;
                     float y = alpha * acc[r][t][e];
-                    if (beta != 0.0f) y += beta * (float)*dst;
+                    if (beta != 0.0f) y += beta * (float)((const TC*)p.epi.cin)[(int64_t)row * p.epi.ldcin + o + e];
+                    if (p.epi.bias) y += vkb::bias_at(p.epi, o + e);
                     *dst = (TC)y;
                 }
             }
@@ -713,6 +718,7 @@ extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const 
                                  uint32_t M, uint32_t N, uint32_t K,
                                  float alpha, float beta, int scalar_mode,
                                  const void* alpha_dev, const void* beta_dev,
+                                 const vkb_epilogue_args* epi,
                                  float* part, uint32_t nsplit, void* stream) {
     if (M == 0 || M > 64 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
     if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) return (int)hipErrorInvalidValue;
@@ -729,6 +735,13 @@ extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const 
     p.M = M; p.N = N; p.K = K;
     p.alpha = alpha; p.beta = beta; p.mode = scalar_mode;
     p.alpha_dev = alpha_dev; p.beta_dev = beta_dev;
+    // a K split writes raw partials: the reduce applies Cin and bias
+    const bool split = nsplit > 1;
+    p.epi.cin = (epi && epi->c_in) ? epi->c_in : C;
+    p.epi.ldcin = (epi && epi->c_in) ? epi->ldc_in : ldc;
+    p.epi.scin = 0;
+    p.epi.bias = (epi && !split) ? epi->bias : nullptr;
+    p.epi.bias_type = epi ? epi->bias_type : 0;
     hipStream_t st = (hipStream_t)stream;
     const bool f32_out = c_type == VKB_T_F32;
     return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, part, (int)nsplit, st)

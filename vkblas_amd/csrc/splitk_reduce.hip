@@ -8,6 +8,7 @@
 // atomics, so results are bitwise reproducible run to run.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "epilogue.hpp"
 #include "vkb_launch.h"
 
 extern "C" int vkb_launch_gemm_f32_impl(const vkb_gemm_args* a, int tile, void* stream);
@@ -15,6 +16,8 @@ extern "C" int vkb_launch_gemm_f16h_impl(const vkb_gemm_args* a, int tile, void*
 extern "C" int vkb_launch_gemm_f16s_impl(const vkb_gemm_args* a, int tile, void* stream);
 extern "C" int vkb_launch_gemm_bf16h_impl(const vkb_gemm_args* a, int tile, void* stream);
 extern "C" int vkb_launch_gemm_bf16s_impl(const vkb_gemm_args* a, int tile, void* stream);
+extern "C" int vkb_launch_gemm_f32h_impl(const vkb_gemm_args* a, int tile, void* stream);
+extern "C" int vkb_launch_gemm_f32b_impl(const vkb_gemm_args* a, int tile, void* stream);
 
 namespace {
 
@@ -31,7 +34,7 @@ template <typename TC>
 __global__ __launch_bounds__(64 * RWAVES) void splitk_reduce_kernel(
     const float* __restrict__ P, int64_t ss, uint32_t split, uint32_t M, uint32_t N,
     TC* __restrict__ C, int64_t ldc, float alpha, float beta, int mode,
-    const void* alpha_dev, const void* beta_dev) {
+    const void* alpha_dev, const void* beta_dev, vkb::EpiParams epi) {
     __shared__ float4 wsum[RWAVES - 1][64];
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t ng = (N + 3) >> 2;
@@ -84,9 +87,11 @@ __global__ __launch_bounds__(64 * RWAVES) void splitk_reduce_kernel(
         beta = (float)*(const _Float16*)beta_dev;
     }
     TC* dst = C + (int64_t)m * ldc + n;
+    const TC* cin = (const TC*)epi.cin + (int64_t)m * epi.ldcin + n;
     for (int e = 0; e < nv; ++e) {
         float y = alpha * acc[e];
-        if (beta != 0.0f) y += beta * (float)dst[e];
+        if (beta != 0.0f) y += beta * (float)cin[e];
+        if (epi.bias) y += vkb::bias_at(epi, (int64_t)n + e);
         put<TC>(dst + e, y);
     }
 }
@@ -96,23 +101,30 @@ __global__ __launch_bounds__(64 * RWAVES) void splitk_reduce_kernel(
 extern "C" int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t split,
                                         uint32_t M, uint32_t N, void* C, int64_t ldc, int c_type,
                                         float alpha, float beta, int scalar_mode,
-                                        const void* alpha_dev, const void* beta_dev, void* stream) {
+                                        const void* alpha_dev, const void* beta_dev,
+                                        const vkb_epilogue_args* ep, void* stream) {
     const uint64_t groups = (uint64_t)M * ((N + 3) / 4);
     const uint64_t blocks = (groups + 63) / 64;
     if (blocks == 0 || blocks > 0x7fffffffull || split == 0) return (int)hipErrorInvalidValue;
     hipStream_t st = (hipStream_t)stream;
+    vkb::EpiParams epi;
+    epi.cin = ep && ep->c_in ? ep->c_in : C;
+    epi.ldcin = ep && ep->c_in ? ep->ldc_in : ldc;
+    epi.scin = 0;
+    epi.bias = ep ? ep->bias : nullptr;
+    epi.bias_type = ep ? ep->bias_type : 0;
     if (c_type == VKB_T_F32) {
         hipLaunchKernelGGL(splitk_reduce_kernel<float>, dim3((uint32_t)blocks), dim3(64 * RWAVES), 0, st, P,
                            stride_split, split, M, N, (float*)C, ldc, alpha, beta, scalar_mode,
-                           alpha_dev, beta_dev);
+                           alpha_dev, beta_dev, epi);
     } else if (c_type == VKB_T_F16) {
         hipLaunchKernelGGL(splitk_reduce_kernel<_Float16>, dim3((uint32_t)blocks), dim3(64 * RWAVES), 0, st, P,
                            stride_split, split, M, N, (_Float16*)C, ldc, alpha, beta, scalar_mode,
-                           alpha_dev, beta_dev);
+                           alpha_dev, beta_dev, epi);
     } else if (c_type == VKB_T_BF16) {
         hipLaunchKernelGGL(splitk_reduce_kernel<__bf16>, dim3((uint32_t)blocks), dim3(64 * RWAVES), 0, st, P,
                            stride_split, split, M, N, (__bf16*)C, ldc, alpha, beta, scalar_mode,
-                           alpha_dev, beta_dev);
+                           alpha_dev, beta_dev, epi);
     } else {
         return (int)hipErrorInvalidValue;
     }
@@ -127,6 +139,8 @@ extern "C" uint32_t vkb_tile_bk(int ab_type) { return ab_type == VKB_T_F32 ? 32u
 
 extern "C" int vkb_launch_gemm(const vkb_gemm_args* a, int tile, void* stream) {
     if (a->ab_type == VKB_T_F32 && a->c_type == VKB_T_F32) return vkb_launch_gemm_f32_impl(a, tile, stream);
+    if (a->ab_type == VKB_T_F32 && a->c_type == VKB_T_F16) return vkb_launch_gemm_f32h_impl(a, tile, stream);
+    if (a->ab_type == VKB_T_F32 && a->c_type == VKB_T_BF16) return vkb_launch_gemm_f32b_impl(a, tile, stream);
     if (a->ab_type == VKB_T_F16 && a->c_type == VKB_T_F16) return vkb_launch_gemm_f16h_impl(a, tile, stream);
     if (a->ab_type == VKB_T_F16 && a->c_type == VKB_T_F32) return vkb_launch_gemm_f16s_impl(a, tile, stream);
     if (a->ab_type == VKB_T_BF16 && a->c_type == VKB_T_BF16) return vkb_launch_gemm_bf16h_impl(a, tile, stream);

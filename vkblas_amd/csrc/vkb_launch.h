@@ -24,6 +24,17 @@ enum { VKB_T_F32 = 0, VKB_T_F16 = 1, VKB_T_BF16 = 2 };
 /* how alpha / beta reach the kernel */
 enum { VKB_SCALAR_HOST = 0, VKB_SCALAR_DEV_F32 = 1, VKB_SCALAR_DEV_F16 = 2 };
 
+/* GEMM kernel that ran (vkb_gemm_args.kernel_out, vkblas_last_kernel) */
+enum {
+    VKB_KERN_NONE = 0,
+    VKB_KERN_GENERIC = 1,          /* gemm_kernel<>, full tiles             */
+    VKB_KERN_GENERIC_CHECKED = 2,  /* gemm_kernel<>, edge handling          */
+    VKB_KERN_PIPE256 = 3,          /* gemm_pipe_kernel, 256x256 tiles       */
+    VKB_KERN_PIPE128 = 4,          /* gemm_pipe_kernel, 128x128, 2 stages   */
+    VKB_KERN_PIPE128_4 = 5,        /* gemm_pipe_kernel, 128x128, 4 stages   */
+    VKB_KERN_SKINNY = 6            /* decode kernels (skinny.hip)           */
+};
+
 /* GEMM tile configurations (block tile BM x BN, 4 waves, BK = 128 bytes) */
 enum {
     VKB_TILE_64  = 0,  /*  64 x  64, waves 2x2 of  32x32 */
@@ -31,6 +42,21 @@ enum {
     VKB_TILE_256 = 2,  /* 256 x 256, waves 2x2 of 128x128 */
     VKB_TILE_COUNT = 3
 };
+
+/* Optional epilogue inputs (every launcher):
+ *   C = alpha * acc + beta * C_in + bias[n]
+ * c_in: the matrix beta scales, of the output's element type, with its own
+ *       leading dimension and batch stride; NULL = C itself (in place).
+ *       Read only when beta != 0.
+ * bias: NULL, or one value per column n of C (bias_type: VKB_T_*), shared by
+ *       every batch, added after alpha / beta and before the one rounding. */
+typedef struct vkb_epilogue_args {
+    const void* c_in;
+    int64_t ldc_in;
+    int64_t stride_c_in;
+    const void* bias;
+    int bias_type;
+} vkb_epilogue_args;
 
 typedef struct vkb_gemm_args {
     const void* A;
@@ -57,6 +83,11 @@ typedef struct vkb_gemm_args {
     /* 1: A, B, C are device arrays of `batch` matrix pointers (stride_* are
      * unused); runs the checked generic kernel, split must be 1 */
     int ptr_array;
+    /* optional: receives the VKB_KERN_* value of the launched kernel */
+    int* kernel_out;
+    /* optional epilogue inputs (NULL: in place, no bias); unused by split-K
+     * pass 1, whose raw partials take no epilogue */
+    const vkb_epilogue_args* epi;
 } vkb_gemm_args;
 
 /* Tile-config properties the dispatcher plans with. */
@@ -65,17 +96,18 @@ uint32_t vkb_tile_bn(int tile);
 /* K granularity of one LDS stage for an element type (128 bytes of K). */
 uint32_t vkb_tile_bk(int ab_type);
 
-/* Blocked MFMA GEMM for all four layouts.  ab_type F32 -> c_type F32;
+/* Blocked MFMA GEMM for all four layouts.  ab_type F32 -> c_type F32, F16 or BF16;
  * ab_type F16 -> c_type F16 or F32; ab_type BF16 -> c_type BF16 or F32. */
 int vkb_launch_gemm(const vkb_gemm_args* a, int tile, void* stream);
 
-/* Split-K pass 2: C = alpha * sum_{s=0}^{split-1} P[s] + beta * C, summed in
- * that fixed order (deterministic).  P[s] is M x N fp32, row pitch N,
- * P[s] = P + s*stride_split. */
+/* Split-K pass 2: C = alpha * sum_{s=0}^{split-1} P[s] + beta * C_in + bias,
+ * summed in that fixed order (deterministic).  P[s] is M x N fp32, row
+ * pitch N, P[s] = P + s*stride_split; epi as vkb_gemm_args.epi. */
 int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t split,
                              uint32_t M, uint32_t N, void* C, int64_t ldc, int c_type,
                              float alpha, float beta, int scalar_mode,
-                             const void* alpha_dev, const void* beta_dev, void* stream);
+                             const void* alpha_dev, const void* beta_dev,
+                             const vkb_epilogue_args* epi, void* stream);
 
 /* Skinny 16-bit GEMM for decode (M <= 64 rows of activations):
  *   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n]
@@ -90,6 +122,7 @@ int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, in
                       uint32_t M, uint32_t N, uint32_t K,
                       float alpha, float beta, int scalar_mode,
                       const void* alpha_dev, const void* beta_dev,
+                      const vkb_epilogue_args* epi,
                       float* part, uint32_t nsplit, void* stream);
 
 #ifdef __cplusplus
