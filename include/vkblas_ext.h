@@ -170,6 +170,38 @@ int vkblas_last_path(void);
  * call launched (split-K: its pass-1 kernel). */
 int vkblas_last_kernel(void);
 
+/*
+ * vkblas_gemm_async that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, plan, kernels and results as
+ * vkblas_gemm_async; the split-K and split-decode partials ([split][M][N]
+ * fp32) go to a fixed per-device scratch array of
+ * vkblas_noalloc_scratch_bytes() (64 MiB) instead of an allocated
+ * workspace.  A call whose partials need more returns VKBLAS_ERR_PARAM
+ * before launching anything (e.g. split_k = 128 on a 1024 x 1024 output).
+ * All calls on one device share its array: calls that overlap in time on
+ * one device (other streams, unordered threads) race and must be ordered by
+ * the caller.
+ */
+vkblas_status_t vkblas_gemm_noalloc_async(
+    vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
+    vkblas_op_t op_a, vkblas_op_t op_b,
+    uint32_t M, uint32_t N, uint32_t K,
+    float alpha,
+    const void* A, uint32_t lda,
+    const void* B, uint32_t ldb,
+    float beta,
+    void* C, uint32_t ldc,
+    uint32_t batch,
+    int64_t stride_a, int64_t stride_b, int64_t stride_c,
+    vkblas_scalar_mode_t scalar_mode, const void* alpha_dev, const void* beta_dev,
+    uint32_t split_k,
+    void* stream);
+
+/* Size in bytes of the per-device scratch array of vkblas_gemm_noalloc_async. */
+size_t vkblas_noalloc_scratch_bytes(void);
+
 /* Frees the split-K / decode partial buffers the library keeps per stream
  * between calls (they are otherwise kept until the process ends, at most
  * 4 GiB in all).  Waits for all work on every device that holds one.  Call

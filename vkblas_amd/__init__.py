@@ -88,6 +88,9 @@ def load():
     L.vkblas_cache_invalidate_base.restype = None
     L.vkblas_last_kernel.restype = _int
     L.vkblas_workspace_release.restype = _int
+    L.vkblas_gemm_noalloc_async.argtypes = L.vkblas_gemm_async.argtypes
+    L.vkblas_gemm_noalloc_async.restype = _int
+    L.vkblas_noalloc_scratch_bytes.restype = ctypes.c_size_t
     _lib = L
     return L
 
@@ -144,6 +147,23 @@ def gemm_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta
     if check and st != OK:
         raise VkblasError(st, "vkblas_gemm_async")
     return st
+
+
+def gemm_noalloc_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1,
+                       stride_a=0, stride_b=0, stride_c=0, scalar_mode=SCALAR_HOST, alpha_dev=None, beta_dev=None,
+                       split_k=0, stream=None, check=True) -> int:
+    """vkblas_gemm_noalloc_async: gemm_async with the partials in the library's
+    per-device scratch array (allocates nothing)."""
+    st = load().vkblas_gemm_noalloc_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C,
+                                          ldc, batch, stride_a, stride_b, stride_c, scalar_mode, alpha_dev, beta_dev,
+                                          split_k, stream)
+    if check and st != OK:
+        raise VkblasError(st, "vkblas_gemm_noalloc_async")
+    return st
+
+
+def noalloc_scratch_bytes() -> int:
+    return load().vkblas_noalloc_scratch_bytes()
 
 
 def gemm_batched_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch,
