@@ -78,6 +78,9 @@ def lib():
         L.oracle_ref_gemm_bf16f32_rm.argtypes = L.oracle_ref_gemm_f16f32_rm.argtypes
         L.oracle_ref_gemm_f32_rm.argtypes = [_int, _int, _int, _int, _int, _f32p, _i64, _f32p, _i64, _flt, _flt,
                                              _f32p, _i64, rows_t, _int, _int]
+        _vp = ctypes.c_void_p
+        L.oracle_ref_gemm_epi_rm.argtypes = [_int, _int, _int, _int, _int, _int, _int, _vp, _i64, _vp, _i64, _flt,
+                                             _flt, _vp, _i64, _vp, _i64, _vp, rows_t, _int, _int]
         _lib = L
     return _lib
 
@@ -189,6 +192,23 @@ def ref_gemm_bf16_rm(op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, 
     """bf16 GEMM (vkblas_gemm_bf16), in place on C (uint16 bf16 patterns, row-major)."""
     p, n, keep = _rows_arg(rows)
     lib().oracle_ref_gemm_bf16_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc, p, n, threads)
+    del keep
+
+
+_TCODE = {"f32": 0, "f16": 1, "bf16": 2}
+
+
+def ref_gemm_epi_rm(ab: str, ct: str, op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, B, ldb: int,
+                    alpha: float, beta: float, Cin, ldcin: int, D, ldd: int, bias=None, rows=None,
+                    threads: int = 0) -> None:
+    """D = alpha * A.B + beta * Cin + bias[n] (hipBLASLt bias epilogue, separate C and D), one rounding to
+    D's type.  ab / ct: "f32", "f16" or "bf16" (16-bit data as uint16 bit patterns); bias: float32 values
+    or None.  In place on D (row-major)."""
+    p, n, keep = _rows_arg(rows)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    lib().oracle_ref_gemm_epi_rm(_TCODE[ab], _TCODE[ct], op_a, op_b, M, N, K, A.ctypes.data, lda, B.ctypes.data,
+                                 ldb, alpha, beta, Cin.ctypes.data, ldcin, D.ctypes.data, ldd,
+                                 None if b is None else b.ctypes.data, p, n, threads)
     del keep
 
 

@@ -49,6 +49,17 @@
  *                          oracle_ref_gemm_f16_rm (double accumulation of the
  *                          exact products, then alpha * (float)s + beta * C).
  *
+ *   oracle_ref_gemm_epi_rm  any of the above input / output types (fp32, fp16,
+ *                          bf16) with the epilogue hipBLASLt defines for its
+ *                          HIPBLASLT_EPILOGUE_BIAS and its separate C and D
+ *                          (no reference counterpart; PyTorch's addmm with a
+ *                          1-D bias, reference test/test_torch.py:65-73,
+ *                          reaches it): D = alpha * (float)s + beta * C_in +
+ *                          bias[n], in fp32, rounded once to D's type; C_in
+ *                          read only if beta != 0; bias (fp32 values, or
+ *                          NULL) indexed by the column n of the row-major
+ *                          result.  Without bias and with C_in == D it is the
+ *                          functions above, bit for bit.
  * The *_omp variants split the same arithmetic over output columns with
  * OpenMP (each output is still computed by one thread in the same order).
  */
@@ -318,6 +329,46 @@ void oracle_ref_gemm_f32_rm(int op_a, int op_b, int M, int N, int K, const float
             }
             float old = beta != 0.0f ? C[(int64_t)m * ldc + n] : 0.0f;
             C[(int64_t)m * ldc + n] = alpha * (float)s + beta * old;
+        }
+    }
+    (void)threads;
+}
+
+/* Element types of oracle_ref_gemm_epi_rm: 0 fp32, 1 fp16, 2 bf16. */
+static float load_t(int t, const void* p, int64_t i) {
+    if (t == 0) return ((const float*)p)[i];
+    h2f_lut_init();
+    const uint16_t h = ((const uint16_t*)p)[i];
+    return t == 1 ? g_h2f_lut[h] : g_bf2f_lut[h];
+}
+
+static void store_t(int t, void* p, int64_t i, float v) {
+    if (t == 0) ((float*)p)[i] = v;
+    else ((uint16_t*)p)[i] = t == 1 ? oracle_f2h_rne(v) : oracle_f2bf_rne(v);
+}
+
+void oracle_ref_gemm_epi_rm(int ab, int ct, int op_a, int op_b, int M, int N, int K, const void* A, int64_t lda,
+                            const void* B, int64_t ldb, float alpha, float beta, const void* Cin, int64_t ldcin,
+                            void* D, int64_t ldd, const float* bias, const int* rows, int nrows, int threads) {
+    int nr = rows ? nrows : M;
+    h2f_lut_init();
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
+#endif
+    for (int ri = 0; ri < nr; ++ri) {
+        for (int n = 0; n < N; ++n) {
+            const int m = rows ? rows[ri] : ri;
+            double s = 0.0;
+            for (int k = 0; k < K; ++k) {
+                float av = load_t(ab, A, op_a ? (int64_t)k * lda + m : (int64_t)m * lda + k);
+                float bv = load_t(ab, B, op_b ? (int64_t)n * ldb + k : (int64_t)k * ldb + n);
+                s += (double)av * bv;
+            }
+            float old = beta != 0.0f ? load_t(ct, Cin, (int64_t)m * ldcin + n) : 0.0f;
+            float v = alpha * (float)s + beta * old;
+            if (bias) v += bias[n];
+            store_t(ct, D, (int64_t)m * ldd + n, v);
         }
     }
     (void)threads;

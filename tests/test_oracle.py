@@ -361,3 +361,100 @@ def test_ref_gemm_bf16_closed_forms_and_planted_mistakes():
     assert not np.array_equal(oracle.bf2f(run(0, beta=0.0)).reshape(M, N), exact.astype(np.float32))
     assert not np.array_equal(oracle.bf2f(run(0, fn=oracle.ref_gemm_f16_rm)).reshape(M, N),
                               exact.astype(np.float32))
+
+
+# ------------------------------------------------------- epilogue (bias, C_in)
+
+def _epi_data(ab, ct, M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    conv = {"f32": lambda x: x.astype(np.float32), "f16": oracle.f2h_rne, "bf16": oracle.f2bf_rne}
+    a = conv[ab](rng.uniform(-1, 1, M * K).astype(np.float32))
+    b = conv[ab](rng.uniform(-1, 1, K * N).astype(np.float32))
+    c = conv[ct](rng.uniform(-1, 1, M * N).astype(np.float32))
+    return a, b, c
+
+
+_TYPES = [("f32", "f32"), ("f32", "f16"), ("f32", "bf16"), ("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"),
+          ("bf16", "f32")]
+
+
+@pytest.mark.parametrize("ab,ct", _TYPES)
+def test_ref_gemm_epi_reduces_to_in_place_oracles(ab, ct):
+    """No bias and C_in == D: the existing restatements, bit for bit."""
+    M, N, K = 13, 17, 29
+    for op_a in (0, 1):
+        for op_b in (0, 1):
+            a, b, c = _epi_data(ab, ct, M, N, K, 7 + op_a + 2 * op_b)
+            lda, ldb = (M if op_a else K), (K if op_b else N)
+            got = c.copy()
+            oracle.ref_gemm_epi_rm(ab, ct, op_a, op_b, M, N, K, a, lda, b, ldb, 0.75, -0.5, got, N, got, N)
+            want = c.copy()
+            if ab == "f32" and ct == "f32":
+                oracle.ref_gemm_f32_rm(op_a, op_b, M, N, K, a, lda, b, ldb, 0.75, -0.5, want, N)
+            elif ab == "f32":
+                # fp32 oracle on the widened C, rounded once
+                back, to = (oracle.h2f, oracle.f2h_rne) if ct == "f16" else (oracle.bf2f, oracle.f2bf_rne)
+                w32 = back(c).astype(np.float32)
+                oracle.ref_gemm_f32_rm(op_a, op_b, M, N, K, a, lda, b, ldb, 0.75, -0.5, w32, N)
+                want = to(w32)
+            else:
+                fn = {("f16", "f16"): oracle.ref_gemm_f16_rm, ("f16", "f32"): oracle.ref_gemm_f16f32_rm,
+                      ("bf16", "bf16"): oracle.ref_gemm_bf16_rm, ("bf16", "f32"): oracle.ref_gemm_bf16f32_rm}
+                fn[(ab, ct)](op_a, op_b, M, N, K, a, lda, b, ldb, 0.75, -0.5, want, N)
+            assert np.array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_ref_gemm_epi_closed_forms():
+    """A = 0: D = beta * C_in + bias exactly (small integers are exact in
+    fp32); C_in separate from D (D's own contents never read); beta == 0
+    never reads C_in (NaN there); bias runs along the columns n."""
+    M, N, K = 5, 7, 3
+    A = np.zeros(M * K, np.float32)
+    B = np.arange(K * N, dtype=np.float32)
+    cin = np.arange(M * N, dtype=np.float32).reshape(M, N)
+    bias = (10 * np.arange(N)).astype(np.float32)
+    D = np.full(M * N, 123.0, np.float32)
+    oracle.ref_gemm_epi_rm("f32", "f32", 0, 0, M, N, K, A, K, B, N, 1.0, 2.0, cin.reshape(-1), N, D, N, bias)
+    assert np.array_equal(D.reshape(M, N), 2.0 * cin + bias[None, :])
+    # beta == 0: C_in is never read, the bias alone remains (plus the product)
+    A1 = np.ones(M * K, np.float32)
+    nan_in = np.full(M * N, np.nan, np.float32)
+    D1 = np.zeros(M * N, np.float32)
+    oracle.ref_gemm_epi_rm("f32", "f32", 0, 0, M, N, K, A1, K, B, N, 1.0, 0.0, nan_in, N, D1, N, bias)
+    want = B.reshape(K, N).sum(axis=0)[None, :] + bias[None, :]
+    assert np.array_equal(D1.reshape(M, N), np.broadcast_to(want, (M, N)))
+    # padded leading dimensions of C_in and D: the padding is untouched
+    ldi, ldd = N + 3, N + 5
+    cin_p = np.full(M * ldi, -1.0, np.float32)
+    cin_p.reshape(M, ldi)[:, :N] = cin
+    D2 = np.full(M * ldd, 77.0, np.float32)
+    oracle.ref_gemm_epi_rm("f32", "f32", 0, 0, M, N, K, A, K, B, N, 1.0, 2.0, cin_p, ldi, D2, ldd, bias)
+    assert np.array_equal(D2.reshape(M, ldd)[:, :N], 2.0 * cin + bias[None, :])
+    assert np.all(D2.reshape(M, ldd)[:, N:] == 77.0)
+
+
+def test_ref_gemm_epi_planted_mistakes_fail():
+    """A bias along the rows, a bias added after the rounding, and C read from
+    D instead of C_in are all distinguishable from the oracle."""
+    M, N, K = 6, 6, 8
+    rng = np.random.default_rng(3)
+    a = oracle.f2h_rne(rng.uniform(-1, 1, M * K).astype(np.float32))
+    b = oracle.f2h_rne(rng.uniform(-1, 1, K * N).astype(np.float32))
+    cin = oracle.f2h_rne(rng.uniform(-1, 1, M * N).astype(np.float32))
+    bias = rng.uniform(-1, 1, N).astype(np.float32) * 1e-3 + np.float32(1.0)
+    D = np.zeros(M * N, np.uint16)
+    oracle.ref_gemm_epi_rm("f16", "f16", 0, 0, M, N, K, a, K, b, N, 1.0, 0.5, cin, N, D, N, bias)
+    # float64 model of the definition
+    A = oracle.h2f(a).astype(np.float64).reshape(M, K)
+    Bm = oracle.h2f(b).astype(np.float64).reshape(K, N)
+    s = (A @ Bm).astype(np.float32)
+    exact = s + np.float32(0.5) * oracle.h2f(cin).reshape(M, N) + bias[None, :]
+    assert np.array_equal(D.reshape(M, N), oracle.f2h_rne(exact.astype(np.float32).reshape(-1)).reshape(M, N))
+    rows_bias = s + np.float32(0.5) * oracle.h2f(cin).reshape(M, N) + bias[:, None]
+    assert not np.array_equal(D, oracle.f2h_rne(rows_bias.astype(np.float32).reshape(-1)))
+    no_bias16 = oracle.f2h_rne((s + np.float32(0.5) * oracle.h2f(cin).reshape(M, N)).astype(np.float32).reshape(-1))
+    late = oracle.f2h_rne((oracle.h2f(no_bias16).reshape(M, N) + bias[None, :]).astype(np.float32).reshape(-1))
+    assert not np.array_equal(D, late)
+    from_d = np.zeros(M * N, np.uint16)
+    oracle.ref_gemm_epi_rm("f16", "f16", 0, 0, M, N, K, a, K, b, N, 1.0, 0.5, from_d, N, from_d, N, bias)
+    assert not np.array_equal(D, from_d)

@@ -43,6 +43,12 @@ class VkblasError(RuntimeError):
         self.status = status
 
 
+class Epilogue(ctypes.Structure):
+    """vkblas_epilogue_t: C = alpha * op(A) op(B) + beta * c_in + bias[n]."""
+    _fields_ = [("c_in", ctypes.c_void_p), ("ldc_in", ctypes.c_uint32), ("stride_c_in", ctypes.c_int64),
+                ("bias", ctypes.c_void_p), ("bias_type", ctypes.c_int)]
+
+
 class Plan(ctypes.Structure):
     _fields_ = [("path", ctypes.c_int), ("tile", ctypes.c_int), ("split", ctypes.c_uint32),
                 ("k_per_split", ctypes.c_uint32)]
@@ -74,6 +80,8 @@ def load():
     L.vkblas_gemm_async.argtypes = [_int, _int, _int, _int, _u32, _u32, _u32, _f, _vp, _u32, _vp, _u32, _f, _vp,
                                     _u32, _u32, _i64, _i64, _i64, _int, _vp, _vp, _u32, _vp]
     L.vkblas_gemm_async.restype = _int
+    L.vkblas_gemm_ex_async.argtypes = L.vkblas_gemm_async.argtypes[:-1] + [ctypes.POINTER(Epilogue), _vp]
+    L.vkblas_gemm_ex_async.restype = _int
     L.vkblas_gemm_batched_async.argtypes = [_int, _int, _int, _int, _u32, _u32, _u32, _f, _vp, _u32, _vp, _u32, _f,
                                             _vp, _u32, _u32, _int, _vp, _vp, _vp]
     L.vkblas_gemm_batched_async.restype = _int
@@ -146,6 +154,21 @@ def gemm_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta
                                   stream)
     if check and st != OK:
         raise VkblasError(st, "vkblas_gemm_async")
+    return st
+
+
+def gemm_ex_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch=1,
+                  stride_a=0, stride_b=0, stride_c=0, scalar_mode=SCALAR_HOST, alpha_dev=None, beta_dev=None,
+                  split_k=0, c_in=None, ldc_in=0, stride_c_in=0, bias=None, bias_type=DT_F32, stream=None,
+                  check=True) -> int:
+    """vkblas_gemm_ex_async: gemm_async with a separate C input (c_in, beta's
+    matrix) and a bias vector (one value per column n of C)."""
+    ep = Epilogue(c_in, ldc_in, stride_c_in, bias, bias_type)
+    st = load().vkblas_gemm_ex_async(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
+                                     batch, stride_a, stride_b, stride_c, scalar_mode, alpha_dev, beta_dev, split_k,
+                                     ctypes.byref(ep), stream)
+    if check and st != OK:
+        raise VkblasError(st, "vkblas_gemm_ex_async")
     return st
 
 
