@@ -42,10 +42,11 @@ def test_library_loads():
     assert L is vk.load()
 
 
-@pytest.mark.parametrize("header", ["vkblas.h", "vkblas_ext.h", "vkblas_hipblas.h", "vkblas_rocblas.h"])
+@pytest.mark.parametrize("header", ["vkblas.h", "vkblas_ext.h", "vkblas_hipblas.h", "vkblas_rocblas.h",
+                                    "vkblas_hipblaslt.h"])
 def test_exports_every_declared_symbol(header):
     names = declared_functions(header)
-    assert len(names) > 3, names
+    assert len(names) >= 3, names
     missing = sorted(names - exported_symbols())
     assert not missing, missing
 
@@ -67,11 +68,32 @@ def test_no_free_interposition():
     assert not ({"hipFree", "hipHostFree", "hipFreeManaged"} & exported_symbols())
 
 
+def _needed(path):
+    out = subprocess.run(["readelf", "-d", path], check=True, capture_output=True, text=True).stdout
+    return re.findall(r"\[(.*?)\]", "\n".join(l for l in out.splitlines() if "NEEDED" in l))
+
+
 def test_no_cuda_or_oracle_dependency():
-    out = subprocess.run(["readelf", "-d", vk.LIB_PATH], check=True, capture_output=True, text=True).stdout
-    needed = re.findall(r"\[(.*?)\]", "\n".join(l for l in out.splitlines() if "NEEDED" in l))
-    assert any(n.startswith("libamdhip64") for n in needed)
-    assert not any("oracle" in n or "cuda" in n or "hipblas" in n or "rocblas" in n for n in needed), needed
+    """The drop-in library depends on no HIP runtime (LD_PRELOADed before an
+    application's own runtime, it must not load one); the engine it opens
+    depends on libamdhip64.so.7 and on nothing of CUDA, the oracle or the
+    vendor BLAS libraries."""
+    shim = _needed(vk.LIB_PATH)
+    assert not any(n.startswith(("libamdhip64", "libhsa")) for n in shim), shim
+    eng = _needed(vk.ENGINE_PATH)
+    assert "libamdhip64.so.7" in eng, eng
+    for needed in (shim, eng):
+        assert not any("oracle" in n or "cuda" in n or "hipblas" in n or "rocblas" in n for n in needed), needed
+
+
+def test_drop_in_references_no_hip_runtime_symbol():
+    """Every HIP call goes through the engine: the drop-in's undefined symbols
+    name no hip* runtime function (hipBLAS / hipBLASLt / rocBLAS ones are
+    resolved at run time and not linked either)."""
+    out = subprocess.run(["nm", "-D", "--undefined-only", vk.LIB_PATH], check=True, capture_output=True,
+                         text=True).stdout
+    undef = {line.split()[-1].split("@")[0] for line in out.splitlines() if line.strip()}
+    assert not {u for u in undef if u.startswith(("hip", "rocblas", "hsa"))}, sorted(undef)
 
 
 # --------------------------------------------------------------- planning
@@ -89,7 +111,7 @@ def test_hip_symbol_versions_within_torch_runtime():
     torch_rt = os.path.join(os.path.dirname(importlib.util.find_spec("torch").origin), "lib", "libamdhip64.so")
     if not os.path.exists(torch_rt):
         pytest.skip("no bundled HIP runtime in this torch")
-    need = set(re.findall(r"\((hip_[0-9.]+)\)", subprocess.run(["objdump", "-T", vk.LIB_PATH], capture_output=True,
+    need = set(re.findall(r"\((hip_[0-9.]+)\)", subprocess.run(["objdump", "-T", vk.ENGINE_PATH], capture_output=True,
                                                                text=True, check=True).stdout))
     have = set(re.findall(r"\b(hip_[0-9.]+)\b", subprocess.run(["objdump", "-T", torch_rt], capture_output=True,
                                                                text=True, check=True).stdout))
@@ -224,20 +246,14 @@ def test_plan_split_heuristic_and_off():
     assert pl.split * pl.k_per_split >= 100 > (pl.split - 1) * pl.k_per_split
 
 
-def test_preload_env_puts_torch_runtime_first():
-    """The preload list leads with torch's own HIP runtime, then this library
-    (two HIP runtimes in one process would not share streams)."""
-    import os
+def test_preload_env_keeps_existing_preloads():
+    """The preload list leads with this library and keeps what the
+    environment already preloads; no HIP runtime is preloaded (the engine
+    binds to the application's own)."""
     from vkblas_amd import preload, LIB_PATH
     env = preload.preload_env(base={"LD_PRELOAD": "/x/other.so"})
-    libs = env["LD_PRELOAD"].split(":")
-    rt = preload.torch_hip_runtime()
-    if rt:
-        assert libs[0] == rt and os.path.basename(rt) == "libamdhip64.so"
-        assert libs[1] == LIB_PATH
-    else:
-        assert libs[0] == LIB_PATH
-    assert libs[-1] == "/x/other.so"
+    assert env["LD_PRELOAD"].split(":") == [LIB_PATH, "/x/other.so"]
+    assert preload.preload_env(base={})["LD_PRELOAD"] == LIB_PATH
     assert preload.main([]) == 2
     assert preload.torch_hipblas_command(["python3", "s.py", "-x"]) == ["python3", "-m", "vkblas_amd.torch_hipblas",
                                                                          "s.py", "-x"]

@@ -1,12 +1,12 @@
 """PyTorch-ROCm with libvkblas_hipblas.so preloaded, the reference's main use
-(reference README.md:56-70, test/test_torch.py): torch's matmul, bmm and
-linear must reach this library's hipBLAS entry points and give the right
-answers.  Each case runs in a child process started with the preload
-environment of vkblas_amd.preload; VKBLAS_TRACE=1 makes the library log every
-GEMM it takes, so the test can tell an intercepted call from one that went to
-the real hipBLAS.  The child selects PyTorch's hipBLAS backend with
-torch.backends.cuda.preferred_blas_library("cublas"), as a PyTorch user of the
-library must on gfx950 (the default there is hipBLASLt).
+(reference README.md:56-70, test/test_torch.py): torch's matmul, bmm, addmm
+and linear must reach this library and give the right answers.  Each case
+runs in a child process with the library in LD_PRELOAD; VKBLAS_TRACE=1 makes
+the library log every GEMM it takes, so the test can tell an intercepted call
+from one that went to the vendor library.  Two backends: PyTorch's default on
+gfx950 (hipBLASLt, interposed at hipblasLtMatmul), and its hipBLAS backend
+(torch.backends.cuda.preferred_blas_library("cublas")), which calls the
+hipBLAS and rocBLAS entry points.
 """
 import json
 import subprocess
@@ -115,3 +115,104 @@ def test_unmodified_script_through_the_runner(tmp_path):
     assert rel <= 1e-5 * 200 ** 0.5
     assert any(l.startswith("[vkblas] hipblas gemm NN f32->f32 m=100 n=300 k=200") for l in r.stderr.splitlines()), \
         r.stderr[-4000:]
+
+
+# The reference's end-to-end script (test/test_torch.py:10-110), run the way
+# its README runs it: LD_PRELOAD naming this library, PyTorch's default
+# BLAS backend (hipBLASLt on gfx950), nothing else changed.  Added: linear
+# with a bias in fp32 / fp16 / bf16 and addmm with a 1-D bias (hipBLASLt's
+# bias epilogue), each checked against PyTorch's CPU result.
+CHILD_PLAIN = r"""
+import json, torch
+torch.manual_seed(42)
+dev = "cuda"
+out = {}
+def diff(got, ref):
+    torch.cuda.synchronize()
+    got = got.cpu().double(); ref = ref.double()
+    return [float((got - ref).abs().max()), float((got - ref).abs().max() / ref.abs().max())]
+# test_torch.py:10-25 shapes, fp32 a @ b
+for (m, n, k) in [(128, 128, 128), (512, 512, 512), (4096, 4096, 4096), (4096, 1024, 4096), (1024, 4096, 4096),
+                  (257, 129, 64), (33, 65, 17), (1, 64, 64), (64, 1, 64), (3, 5, 7)]:
+    a = torch.randn(m, k, device=dev); b = torch.randn(k, n, device=dev)
+    out[f"mm_{m}x{n}x{k}"] = diff(a @ b, a.cpu() @ b.cpu())
+# :28-34 bmm
+a = torch.randn(4, 64, 32, device=dev); b = torch.randn(4, 32, 128, device=dev)
+out["bmm"] = diff(torch.bmm(a, b), torch.bmm(a.cpu(), b.cpu()))
+# :37-43 x @ W.t()
+x = torch.randn(128, 256, device=dev); w = torch.randn(512, 256, device=dev)
+out["x_wt"] = diff(x @ w.t(), x.cpu() @ w.cpu().t())
+# :45-54 non-contiguous x.t() @ w
+for (M, K, N) in [(33, 97, 65), (128, 256, 128), (512, 768, 256)]:
+    x = torch.randn(K, M, device=dev); w = torch.randn(K, N, device=dev)
+    out[f"xt_w_{M}x{K}x{N}"] = diff(x.t() @ w, x.t().cpu() @ w.cpu())
+# :56-63 batched transposed A
+x = torch.randn(3, 256, 320, device=dev); w = torch.randn(3, 256, 128, device=dev)
+out["bmm_xt_w"] = diff(x.transpose(1, 2) @ w, x.transpose(1, 2).cpu() @ w.cpu())
+# :65-73 addmm with a 1-D bias, alpha / beta
+x = torch.randn(256, 320, device=dev); w = torch.randn(256, 128, device=dev); bias = torch.randn(128, device=dev)
+out["addmm_bias_ab"] = diff(torch.addmm(bias, x.t(), w, beta=0.5, alpha=2.5),
+                            0.5 * bias.cpu() + 2.5 * (x.t().cpu() @ w.cpu()))
+# :75-83 addmm with a matrix C
+a = torch.randn(256, 256, device=dev); b = torch.randn(256, 256, device=dev); c = torch.randn(256, 256, device=dev)
+out["addmm_c"] = diff(torch.addmm(c, a, b, beta=0.7, alpha=0.5), 0.7 * c.cpu() + 0.5 * (a.cpu() @ b.cpu()))
+# :85-91 fp16
+a16 = torch.randn(128, 128, device=dev, dtype=torch.float16); b16 = torch.randn(128, 128, device=dev, dtype=torch.float16)
+out["mm_f16"] = diff(a16 @ b16, a16.cpu().float() @ b16.cpu().float())
+# :93-110 complex128 (forwarded to the vendor library)
+for (m, n, k) in [(16, 16, 16), (33, 65, 17), (128, 256, 320), (512, 256, 768)]:
+    a = torch.randn(m, k, device=dev, dtype=torch.complex128); b = torch.randn(k, n, device=dev, dtype=torch.complex128)
+    torch.cuda.synchronize()
+    d = float((a @ b).cpu().sub(a.cpu() @ b.cpu()).abs().max())
+    out[f"z64_{m}x{n}x{k}"] = [d, d]
+a = torch.randn(3, 64, 32, device=dev, dtype=torch.complex128); b = torch.randn(3, 32, 48, device=dev, dtype=torch.complex128)
+d = float(torch.bmm(a, b).cpu().sub(torch.bmm(a.cpu(), b.cpu())).abs().max()); out["z64_bmm"] = [d, d]
+x = torch.randn(64, 128, device=dev, dtype=torch.complex128); w = torch.randn(256, 128, device=dev, dtype=torch.complex128)
+d = float((x @ w.t()).cpu().sub(x.cpu() @ w.cpu().t()).abs().max()); out["z64_linear"] = [d, d]
+# linear with a bias (addmm + hipBLASLt bias epilogue), three dtypes
+for name, dt in (("f32", torch.float32), ("f16", torch.float16), ("bf16", torch.bfloat16)):
+    x = (torch.randn(64, 512, device=dev) / 16).to(dt); W = torch.randn(384, 512, device=dev).to(dt)
+    b = torch.randn(384, device=dev).to(dt)
+    out[f"linear_bias_{name}"] = diff(torch.nn.functional.linear(x, W, b),
+                                      x.cpu().double() @ W.cpu().double().t() + b.cpu().double())
+    xd = torch.randn(4, 512, device=dev).to(dt)      # decode-shaped
+    out[f"linear_bias_decode_{name}"] = diff(torch.nn.functional.linear(xd, W, b),
+                                             xd.cpu().double() @ W.cpu().double().t() + b.cpu().double())
+print("RESULT " + json.dumps(out), flush=True)
+"""
+
+
+def test_plain_ld_preload_reference_script():
+    """LD_PRELOAD=libvkblas_hipblas.so python script.py, the reference's
+    usage (README.md:60-70), with its test_torch.py cases: every fp32 / fp16
+    / bf16 product reaches this library through hipblasLtMatmul (bias
+    epilogues included) and matches PyTorch's CPU result; complex128 goes to
+    the vendor library and is exact to 1e-8 as the reference requires."""
+    import os
+    import vkblas_amd as vk
+    old = os.environ.get("LD_PRELOAD", "")
+    # this library first; whatever the environment already preloads stays
+    env = dict(os.environ, LD_PRELOAD=":".join([vk.LIB_PATH] + ([old] if old else [])), VKBLAS_TRACE="1")
+    print("[case] plain LD_PRELOAD, reference test_torch.py cases", flush=True)
+    r = subprocess.run([sys.executable, "-c", CHILD_PLAIN], env=env, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-4000:]
+    res = json.loads(next(l for l in r.stdout.splitlines() if l.startswith("RESULT "))[len("RESULT "):])
+    for key, (absd, rel) in res.items():
+        if key.startswith("z64"):
+            assert absd < 1e-8, (key, absd)                 # test_torch.py:100
+        elif "bf16" in key:
+            assert rel <= 8e-3, (key, rel)
+        elif "f16" in key:
+            assert rel <= 2e-3, (key, rel)
+        else:
+            assert absd < 0.1, (key, absd)                  # test_torch.py:19
+    err = r.stderr.splitlines()
+    lt = [l for l in err if l.startswith("[vkblas] hipblaslt matmul")]
+    assert len(lt) >= 20, r.stderr[-4000:]
+    assert sum(" bias" in l for l in lt) >= 6, lt           # six linear(x, W, b) calls
+    assert any("f16->f16" in l and " bias" in l for l in lt), lt
+    assert any("bf16->bf16" in l and " bias" in l for l in lt), lt
+    assert any("f32->f32" in l and "m=4096 n=4096 k=4096" in l for l in lt), lt
+    assert not any("forwarding" in l for l in err), r.stderr[-4000:]
+    # the kernels ran in the same process, on PyTorch's HIP runtime
+    assert any(l.startswith("[vkblas] gemm ") and "path=skinny" in l for l in err), r.stderr[-4000:]

@@ -21,6 +21,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 REPO = os.path.dirname(HERE)
 LIB_NAME = "libvkblas_hipblas.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
+# the host dispatcher and kernels, opened by LIB_PATH's first call
+ENGINE_PATH = os.path.join(HERE, "libvkblas_engine.so")
 
 # vkblas_status_t (reference src/vkblas.h:6-12)
 OK, ERR_INIT, ERR_IMPORT, ERR_PARAM, ERR_FALLBACK = 0, 1, 2, 3, 4
@@ -70,8 +72,9 @@ def load():
     global _lib
     if _lib is not None:
         return _lib
-    if not os.path.exists(LIB_PATH):
-        raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() (make -C vkblas_amd)")
+    for path in (LIB_PATH, ENGINE_PATH):
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run __graft_entry__.build() (make -C vkblas_amd)")
     L = ctypes.CDLL(LIB_PATH)
     for name in ("vkblas_gemm_f32", "vkblas_gemm_f16", "vkblas_gemm_bf16", "vkblas_gemm_bf16_hipblas"):
         fn = getattr(L, name)

@@ -13,8 +13,8 @@
  *   - asynchronous on the handle's stream (rocblas_get_stream), no host sync
  *     (reference line 867);
  *   - rocblas_pointer_mode_device scalars are read by the kernels;
- *   - a D distinct from C is supported (C is copied into D on the stream when
- *     beta may be nonzero; with beta == 0 C is never read); the reference
+ *   - a D distinct from C is supported (the kernels read beta's matrix from
+ *     C and write D; with beta == 0 C is never read); the reference
  *     forwarded c != d (line 838);
  *   - fp16 inputs with fp32 C / D are computed too;
  *   - m, n, k or batch_count <= 0 and invalid leading dimensions are forwarded
@@ -189,18 +189,16 @@ static int run(const gemm_call* g) {
                 (long long)g->m, (long long)g->n, (long long)g->k,
                 (long long)g->lda, (long long)g->ldb, (long long)g->ldc, (long long)g->ldd, (long long)g->batch);
 
-    /* D separate from C: bring C into D first when the epilogue may read it
+    /* D separate from C: the kernels read beta's matrix from C and write D
      * (with pointer arrays the matrices are not known on the host: declined) */
     if (g->ptr_array && g->c != g->d) return 1;
+    vkblas_epilogue_t epi;
+    memset(&epi, 0, sizeof(epi));
     if (!g->ptr_array && g->c != g->d && beta_maybe_nonzero) {
         if (!g->c) return 1;
-        const size_t es = ct == VKBLAS_DT_F32 ? 4 : 2;
-        for (int64_t i = 0; i < g->batch; ++i) {
-            if (hipMemcpy2DAsync((char*)g->d + (size_t)(i * g->sd) * es, (size_t)g->ldd * es,
-                                 (const char*)g->c + (size_t)(i * g->sc) * es, (size_t)g->ldc * es,
-                                 (size_t)g->m * es, (size_t)g->n, hipMemcpyDeviceToDevice, stream) != hipSuccess)
-                return 1;
-        }
+        epi.c_in = g->c;
+        epi.ldc_in = (uint32_t)g->ldc;
+        epi.stride_c_in = g->batch > 1 ? g->sc : 0;
     }
     const vkblas_op_t op_a = op_t(g->transB) ? VKBLAS_OP_T : VKBLAS_OP_N;
     const vkblas_op_t op_b = op_t(g->transA) ? VKBLAS_OP_T : VKBLAS_OP_N;
@@ -211,10 +209,10 @@ static int run(const gemm_call* g) {
                                        (uint32_t)g->lda, beta, (void* const*)g->d, (uint32_t)g->ldd,
                                        (uint32_t)g->batch, sm, ad, bd, stream);
     else
-        st = vkblas_gemm_async(ab, ct, op_a, op_b, (uint32_t)g->n, (uint32_t)g->m, (uint32_t)g->k, alpha, g->b,
-                               (uint32_t)g->ldb, g->a, (uint32_t)g->lda, beta, g->d, (uint32_t)g->ldd,
-                               (uint32_t)g->batch, g->batch > 1 ? g->sb : 0, g->batch > 1 ? g->sa : 0,
-                               g->batch > 1 ? g->sd : 0, sm, ad, bd, 0, stream);
+        st = vkblas_gemm_ex_async(ab, ct, op_a, op_b, (uint32_t)g->n, (uint32_t)g->m, (uint32_t)g->k, alpha, g->b,
+                                  (uint32_t)g->ldb, g->a, (uint32_t)g->lda, beta, g->d, (uint32_t)g->ldd,
+                                  (uint32_t)g->batch, g->batch > 1 ? g->sb : 0, g->batch > 1 ? g->sa : 0,
+                                  g->batch > 1 ? g->sd : 0, sm, ad, bd, 0, epi.c_in ? &epi : NULL, stream);
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return 1;

@@ -1,21 +1,19 @@
-"""Run a program with libvkblas_hipblas.so interposed on hipBLAS (LD_PRELOAD).
+"""Run a program with libvkblas_hipblas.so interposed (LD_PRELOAD).
 
 The reference is used as ``LD_PRELOAD=libvkblas_hipblas.so python script.py``
-(reference README.md:56-70).  Under PyTorch-ROCm one more library has to lead
-the preload list: torch ships its own HIP runtime (``torch/lib/libamdhip64.so``,
-soname ``libamdhip64.so.7``) and loads it by the name ``libamdhip64.so``.  If
-this library were preloaded alone it would pull in the system runtime
-(``/opt/rocm/lib/libamdhip64.so.7``) first and the process would end up with
-two HIP runtimes, whose streams and handles do not mix.  Preloading torch's
-runtime first makes the library bind to that copy (matching soname), and
-torch's later load of the same file is then a no-op.
+(reference README.md:56-70), and so is this library: the preloaded library
+depends on no HIP runtime, and the engine it opens at the first GEMM binds to
+the runtime the application loaded (PyTorch's bundled one, by soname).  On
+gfx950 PyTorch's GEMMs go to hipBLASLt by default, whose hipblasLtMatmul this
+library interposes (bias epilogues included); fp32 / fp16 / bf16 products
+and linear layers therefore reach it with no change to the script.
 
-hipBLAS must also be the BLAS backend PyTorch calls.  On gfx950 PyTorch's
-default heuristic picks hipBLASLt, which this library does not intercept, and
-no environment variable selects hipBLAS (``TORCH_BLAS_PREFER_HIPBLASLT`` can
-only select hipBLASLt).  A script selects it with
-``torch.backends.cuda.preferred_blas_library("cublas")``; ``--torch-hipblas``
-runs an unmodified Python script with that call made first.
+This runner only builds that environment (this library ahead of whatever
+the environment already preloads).  ``--torch-hipblas`` additionally makes
+PyTorch use its hipBLAS backend instead of hipBLASLt (PyTorch then calls the
+hipBLAS and rocBLAS entry points, as on the reference's gfx803), by making
+``torch.backends.cuda.preferred_blas_library("cublas")`` before running an
+unmodified Python script.
 
   python -m vkblas_amd.preload -- python my_script.py [args...]
   python -m vkblas_amd.preload --torch-hipblas -- python my_script.py [args...]
@@ -30,29 +28,14 @@ import sys
 from . import LIB_PATH
 
 
-def torch_hip_runtime() -> str | None:
-    """Path of the HIP runtime bundled with the installed torch, if any (found
-    without importing torch, so no GPU is initialised here)."""
-    import importlib.util
-    spec = importlib.util.find_spec("torch")
-    if spec is None or not spec.origin:
-        return None
-    path = os.path.join(os.path.dirname(spec.origin), "lib", "libamdhip64.so")
-    return path if os.path.exists(path) else None
-
-
-def preload_env(base: dict | None = None, with_torch_runtime: bool = True) -> dict:
-    """Environment for a child process with the library preloaded."""
+def preload_env(base: dict | None = None) -> dict:
+    """Environment for a child process with the library preloaded (ahead of
+    anything the environment already preloads, which stays)."""
     env = dict(os.environ if base is None else base)
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is missing: build it first (make -C vkblas_amd)")
-    libs = []
-    rt = torch_hip_runtime() if with_torch_runtime else None
-    if rt:
-        libs.append(rt)
-    libs.append(LIB_PATH)
     old = env.get("LD_PRELOAD", "")
-    env["LD_PRELOAD"] = ":".join(libs + ([old] if old else []))
+    env["LD_PRELOAD"] = ":".join([LIB_PATH] + ([old] if old else []))
     return env
 
 
