@@ -12,7 +12,8 @@ fp16 MFMA peak, 8192x8192 fp16 decode matvec vs HBM peak, with three weight
 copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fp32|fp16|bf16|matvec|bf16mv|splitk|batched|ceiling|vendor]
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+                  [--only fp32|fp16|bf16|matvec|bf16mv|f32mv|splitk|batched|ceiling|vendor]
 """
 import argparse
 import json
@@ -185,6 +186,34 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
     return out
 
 
+def matvec_f32(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16)):
+    """fp32 decode (the reference's fp32 matvec, src/vkblas.c:2100-2143):
+    Y[ntok][O] = X[ntok][K] . W with W
+    stored O x K (engine op_b = T, hipBLAS TN) and K x O (op_b = N, hipBLAS
+    NN); three weight copies (3 x 256 MiB > 256 MB MALL) rotated per launch."""
+    g = torch.Generator(device="cuda:0").manual_seed(17)
+    Ws = [torch.randn(O * K, device="cuda:0", generator=g) * 0.02 for _ in range(3)]
+    X = torch.randn(max(ntoks) * K, device="cuda:0", generator=g)
+    Y = torch.empty(max(ntoks) * O, device="cuda:0")
+    sp = stream.cuda_stream
+    out = {}
+    for name, ob in (("OxK", vk.OP_T), ("KxO", vk.OP_N)):
+        ldw = K if ob == vk.OP_T else O
+        for nt in ntoks:
+            def call(i):
+                vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, ob, nt, O, K, 1.0, X.data_ptr(), K,
+                              Ws[i % 3].data_ptr(), ldw, 0.0, Y.data_ptr(), O, stream=sp)
+            for i in range(6):
+                call(i)
+            med = batch_ms(torch, stream, call, 3 * max(steps, 10))
+            nbytes = 4 * O * K + 4 * K * nt + 4 * O * nt
+            gbs = nbytes / (med * 1e-3) / 1e9
+            out[f"{name}_n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(gbs, 1),
+                                    "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                                    "path": vk.PATH_NAMES[vk.last_path()]}
+    return out
+
+
 def mfma_ceiling(torch, vk, stream, steps):
     """The v_mfma_f32_16x16x32 rate the chip sustains with no memory traffic
     (vkblas_mfma_probe: the GEMM inner loop's MFMA pattern without its loads),
@@ -252,8 +281,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "splitk", "batched", "calibrate",
-                                       "ceiling", "vendor"],
+    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "f32mv", "splitk", "batched",
+                                       "calibrate", "ceiling", "vendor"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -279,6 +308,11 @@ def main():
         return
     if args.only == "bf16mv":
         print(json.dumps(matvec(torch, vk, stream, args.steps, bf16=True)))
+        return
+    if args.only == "f32mv":
+        print(json.dumps({"8192x8192": matvec_f32(torch, vk, stream, args.steps),
+                          "4096x14336": matvec_f32(torch, vk, stream, args.steps, K=4096, O=14336),
+                          "14336x4096": matvec_f32(torch, vk, stream, args.steps, K=14336, O=4096)}))
         return
     if args.only == "splitk":
         print(json.dumps(splitk(torch, vk, stream, args.steps)))
@@ -347,6 +381,8 @@ def main():
     line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 4, 8, 16))
     log("[bench] decode 8192x8192, 24-64 tokens")
     line["fp16_decode_8192_wide"] = matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))
+    log("[bench] fp32 matvec 8192x8192, both weight layouts")
+    line["fp32_matvec_8192"] = matvec_f32(torch, vk, stream, args.steps)
     log("[bench] split-K and strided-batched")
     line["splitk_256x256"] = splitk(torch, vk, stream, args.steps, splits=(0,))
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)

@@ -134,9 +134,10 @@ def test_plan_rejects_bad_arguments():
         P(vk.DT_F16, vk.DT_BF16, 0, 0, 4, 4, 4, 4, 4, 4)         # f16 in, bf16 out: unsupported
     with pytest.raises(vk.VkblasError):
         P(vk.DT_BF16, vk.DT_F16, 0, 0, 4, 4, 4, 4, 4, 4)         # bf16 in, f16 out: unsupported
-    # fp32 in, 16-bit out (GemmEx 32F/32F/16F and 16BF): a tile path
+    # fp32 in, 16-bit out (GemmEx 32F/32F/16F and 16BF): a tile path (20
+    # rows: more than the fp32 skinny kernels take)
     for ct in (vk.DT_F32, vk.DT_F16, vk.DT_BF16):
-        assert P(vk.DT_F32, ct, 0, 0, 4, 4, 4, 4, 4, 4).path == vk.PATH_TILE64
+        assert P(vk.DT_F32, ct, 0, 0, 20, 4, 4, 4, 4, 4).path == vk.PATH_TILE64
 
 
 def test_engine_param_errors_without_gpu():
@@ -168,10 +169,9 @@ def test_plan_headline_configs():
             assert pl.path == vk.PATH_SKINNY
     # 65 tokens: a GEMM again
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
-    # not skinny when misaligned, batched, or fp32
+    # not skinny when misaligned or batched
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, aligned=False).path != vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192, batch=2).path != vk.PATH_SKINNY
-    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     # config 5b: batched 64 x 512^3
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 512, 512, 512, 512, 512, 512, batch=64).split == 1
 
@@ -197,6 +197,39 @@ def test_plan_decode_split():
     assert split(20, 128, 100, ld=104) == 1   # a single (partial) K step
 
 
+def test_plan_skinny_f32():
+    """fp32 with up to 16 activation rows (op_a = N, fp32 output): the skinny
+    kernels for W stored N x K (op_b = T, no split) and K x N (op_b = N, N a
+    multiple of 4, K split in whole 64-row groups so that the grid holds
+    about 512 workgroups of 256 columns, each slice at least 8 groups)."""
+    for M in (1, 2, 4, 9, 16):
+        for ob in (0, 1):
+            pl = P(vk.DT_F32, vk.DT_F32, 0, ob, M, 8192, 8192, 8192, 8192, 8192)
+            assert pl.path == vk.PATH_SKINNY
+            assert pl.split == (1 if ob else 16)     # 32 column blocks x 16 slices
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 16, 4096, 14336, 14336, 4096, 4096).split == 28
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 14336, 4096, 4096, 14336, 14336).split == 8
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 1024, 65536, 65536, 1024, 1024).split == 64
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 3, 8192, 1000, 1000, 8192, 8192).split == 2
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 4, 1, 4, 4, 4).split == 1
+    # not skinny: 17 rows, 16-bit output, N % 4 (K x N), op_a = T, misaligned
+    # leading dimensions, ldb short of N
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8190, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 1, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 4, 8192, 8190, 8190, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8192, 8192, 8192, 8188, 8192).path != vk.PATH_SKINNY
+    # one activation row: its leading dimension is never used
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 1, 8192, 8192, 3, 8192, 8192).path == vk.PATH_SKINNY
+    # the staged N x K kernel's 32-bit buffer spans (32 weight rows of ldb)
+    big = (1 << 31) // (32 * 4)
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 4, 4096, 4096, 4096, big - 4, 4096).path == vk.PATH_SKINNY
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 4, 4096, 4096, 4096, big, 4096).path != vk.PATH_SKINNY
+    # the K x N kernel indexes with 64-bit offsets: no span limit
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 4096, 4096, 4096, 1 << 30, 4096).path == vk.PATH_SKINNY
+
+
 def test_plan_decode_span_limit():
     """The decode kernels address a 32-row weight tile and the activation
     rows with 32-bit buffer offsets; a decode-shaped call whose leading
@@ -205,10 +238,15 @@ def test_plan_decode_span_limit():
     big = (1 << 31) // (32 * 2)              # 32 rows of ldb fp16 elements reach 2 GiB
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 4096, 4096, 4096, big - 8, 4096).path == vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 4, 4096, 4096, 4096, big, 4096).path != vk.PATH_SKINNY
-    # activations: 16 rows (M <= 16) or 16 ceil(M / 16) rows of lda
-    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, (1 << 26) - 8, 4096, 4096).path == vk.PATH_SKINNY
-    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, 1 << 26, 4096, 4096).path != vk.PATH_SKINNY
-    assert P(vk.DT_BF16, vk.DT_BF16, 0, 1, 17, 4096, 4096, 1 << 25, 4096, 4096).path != vk.PATH_SKINNY
+    # activations: rows past M repeat row M - 1, so the span is (r - 1) lda
+    # + K elements with r = M (M <= 16) or 16 ceil(M / 16) (counted as the
+    # tiles the decode kernel stages, a bound on M)
+    lim16 = ((1 << 30) - 4096) // 15 // 8 * 8   # largest lda with (15 lda + 4096) 2 bytes < 2 GiB
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, lim16, 4096, 4096).path == vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 16, 4096, 4096, lim16 + 8, 4096, 4096).path != vk.PATH_SKINNY
+    lim32 = ((1 << 30) - 4096) // 31 // 8 * 8
+    assert P(vk.DT_BF16, vk.DT_BF16, 0, 1, 17, 4096, 4096, lim32, 4096, 4096).path == vk.PATH_SKINNY
+    assert P(vk.DT_BF16, vk.DT_BF16, 0, 1, 17, 4096, 4096, lim32 + 8, 4096, 4096).path != vk.PATH_SKINNY
 
 
 @pytest.mark.parametrize("K", [65536, 262144])

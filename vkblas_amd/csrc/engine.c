@@ -341,19 +341,21 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (lda == 0 || ldb == 0 || ldc == 0) return VKBLAS_ERR_PARAM;
     if (split_k == 0 && g_force_split) split_k = g_force_split;
 
-    /* decode-shaped fp16 / bf16: X[M<=64, K] . W[N, K]^T, both K-contiguous.
-     * The decode kernels address a 32-row weight tile and up to 64
-     * activation rows with 32-bit buffer offsets: larger spans take the
-     * tile path (the same bound vkb_launch_skinny enforces). */
-    const uint64_t dec_xrows = M <= 16 ? M : 16 * (((uint64_t)M + 15) / 16);
-    if ((ab_type == VKBLAS_DT_F16 || ab_type == VKBLAS_DT_BF16) && op_a == VKBLAS_OP_N && op_b == VKBLAS_OP_T && M <= 64 &&
-        batch == 1 && split_k <= 1 && aligned && (lda % 8) == 0 && (ldb % 8) == 0 && lda >= K && ldb >= K &&
-        (uint64_t)32 * ldb * 2 < (1ull << 31) && dec_xrows * lda * 2 < (1ull << 31) && !g_no_skinny) {
-        plan->path = VKBLAS_PATH_SKINNY;
-        plan->tile = VKB_TILE_64;
-        plan->split = vkb_skinny_split(M, N, K);
-        plan->k_per_split = K;   /* the decode kernel splits whole K steps itself */
-        return VKBLAS_OK;
+    /* decode-shaped: X[M, K] (K-contiguous rows) against a weight W.
+     * fp16 / bf16: M <= 64, W stored N x K (op_b = T); fp32: M <= 16, W
+     * stored N x K or K x N, fp32 output.  vkb_skinny_plan holds the
+     * kernels' own limits (leading dimensions, 32-bit buffer spans) and
+     * returns their K split, or 0: then a tile path. */
+    if (op_a == VKBLAS_OP_N && batch == 1 && split_k <= 1 && aligned && !g_no_skinny &&
+        (ab_type != VKBLAS_DT_F32 || c_type == VKBLAS_DT_F32)) {
+        const uint32_t sp = vkb_skinny_plan(kernel_type(ab_type), op_b == VKBLAS_OP_T, M, N, K, lda, ldb);
+        if (sp) {
+            plan->path = VKBLAS_PATH_SKINNY;
+            plan->tile = VKB_TILE_64;
+            plan->split = sp;
+            plan->k_per_split = K;   /* the skinny kernels split K themselves */
+            return VKBLAS_OK;
+        }
     }
 
     const uint32_t bk = vkb_tile_bk(kernel_type(ab_type));
@@ -578,8 +580,9 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
 
     if (plan.path == VKBLAS_PATH_SKINNY) {
         /* decode; with a K split over workgroups: fp32 partials, fixed-order reduce */
-        rc = vkb_launch_skinny(ab, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta, (int)scalar_mode, alpha_dev,
-                               beta_dev, epp, partials ? (float*)ws : NULL, partials ? plan.split : 1, stream);
+        rc = vkb_launch_skinny(ab, op_b == VKBLAS_OP_T, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta,
+                               (int)scalar_mode, alpha_dev, beta_dev, epp, partials ? (float*)ws : NULL,
+                               partials ? plan.split : 1, stream);
         if (rc == 0 && partials)
             rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
                                           (int)scalar_mode, alpha_dev, beta_dev, epp, stream);

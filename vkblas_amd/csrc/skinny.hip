@@ -47,6 +47,42 @@ __device__ __forceinline__ floatx4 mfma16(u32x4 a, u32x4 b, floatx4 c) {
                                                       __builtin_bit_cast(half8_t, b), c, 0, 0, 0);
 }
 
+// The MFMAs of one 16-byte fragment pair (lane group g = lane / 16 holds the
+// g-th 16 bytes of a 64-byte k slice for its row): 16-bit types one
+// v_mfma_f32_16x16x32 (8 k per lane), fp32 four v_mfma_f32_16x16x4_f32, the
+// c-th taking element c of every lane's 4 (k = 4 g + c: each k of the slice
+// exactly once, in the same order for both operands).
+template <typename T>
+__device__ __forceinline__ floatx4 mfma_frag(u32x4 a, u32x4 b, floatx4 c) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]), c, 0, 0, 0);
+        return c;
+    } else {
+        return mfma16<T>(a, b, c);
+    }
+}
+
+// 16 bytes of T elements from p, element i zero unless i < nvalid
+template <typename T>
+__device__ __forceinline__ u32x4 ld16_checked(const T* p, int nvalid) {
+    if (nvalid >= (int)(16 / sizeof(T))) return *(const u32x4*)p;
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if constexpr (sizeof(T) == 4) {
+        const uint32_t* q = (const uint32_t*)p;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (i < nvalid) w[i] = q[i];
+    } else {
+        const uint16_t* q = (const uint16_t*)p;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (i < nvalid) w[i >> 1] |= (uint32_t)q[i] << (16 * (i & 1));
+    }
+    return u32x4{w[0], w[1], w[2], w[3]};
+}
+
 // a + w.lo * x.lo + w.hi * x.hi (v_dot2_f32_f16 / v_dot2c_f32_bf16)
 template <typename T>
 __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float a) {
@@ -92,8 +128,8 @@ __host__ __device__ inline DecPlan dec_plan(uint32_t N, uint32_t K) {
 }
 
 struct SkParams {
-    const uint16_t* X;   // 16-bit elements (fp16 or bf16 bit patterns)
-    const uint16_t* W;
+    const void* X;       // elements of the input type (fp32, or fp16 / bf16 bits)
+    const void* W;
     void* C;
     int64_t lda, ldb, ldc;
     uint32_t M, N, K;
@@ -103,15 +139,6 @@ struct SkParams {
     const void* beta_dev;
     vkb::EpiParams epi;   // Cin (beta's matrix) and bias per output column o
 };
-
-__device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
-    if (nvalid >= 8) return *(const u32x4*)p;
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        if (i < nvalid) w[i >> 1] |= (uint32_t)p[i] << (16 * (i & 1));
-    return u32x4{w[0], w[1], w[2], w[3]};
-}
 
 // ------------------------------------------------------- staged skinny
 // For 3 <= M <= 16 activation rows, full-line loads.  Loading the MFMA
@@ -140,10 +167,12 @@ __device__ __forceinline__ u32x4 ld8_checked(const uint16_t* p, int nvalid) {
 // partial last step (K % 128) goes through plain checked loads.
 template <typename T, typename TC, int XR, int S, int R, int WAVES = 4>
 __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
+    constexpr int ES = sizeof(T);                   // element bytes: 2, or 4 for fp32
+    constexpr int KS = 256 / ES;                    // elements of a 256-byte K step
     constexpr int NQX = XR / 4, NQ = 4 * R + NQX;   // copies per step
     constexpr int WR = 16 * R;                      // weight rows per workgroup
     constexpr int STG = (WR + XR) * 256;            // stage bytes
-    static_assert(XR == 8 || XR == 16, "activation rows staged: 8 or 16");
+    static_assert(XR == 4 || XR == 8 || XR == 16, "activation rows staged: 4, 8 or 16");
     static_assert(S >= 2 && S <= 4 && (S - 1) * NQ < 64 && WAVES * S * STG <= 160 * 1024, "stages");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[WAVES * S * STG];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -152,7 +181,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
     const int n0 = blockIdx.x * WR;
     const int rows_here = min(WR, (int)p.N - n0);
 
-    const int nfull = (int)(p.K / 128);
+    const int nfull = (int)(p.K / KS);
     const int per = (nfull + WAVES - 1) / WAVES;
     const int c_beg = min(nfull, wave * per);
     const int n = min(nfull, c_beg + per) - c_beg;   // wave-uniform
@@ -164,18 +193,20 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
                      __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
     };
     // ranges: the operands' read domains
-    const i32x4 rw = rsrc_words(p.W + (int64_t)n0 * p.ldb, ((int64_t)(rows_here - 1) * p.ldb + p.K) * 2);
-    const i32x4 rx = rsrc_words(p.X, ((int64_t)(p.M - 1) * p.lda + p.K) * 2);
+    const T* Wt = (const T*)p.W;
+    const T* Xt = (const T*)p.X;
+    const i32x4 rw = rsrc_words(Wt + (int64_t)n0 * p.ldb, ((int64_t)(rows_here - 1) * p.ldb + p.K) * ES);
+    const i32x4 rx = rsrc_words(Xt, ((int64_t)(p.M - 1) * p.lda + p.K) * ES);
     int vw[4 * R], vx[NQX];
 #pragma unroll
     for (int q = 0; q < 4 * R; ++q) {
         const int row = 4 * q + g;
-        vw[q] = (int)((int64_t)min(row, rows_here - 1) * p.ldb * 2) + ((l16 ^ (row & 15)) << 4);
+        vw[q] = (int)((int64_t)min(row, rows_here - 1) * p.ldb * ES) + ((l16 ^ (row & 15)) << 4);
     }
 #pragma unroll
     for (int q = 0; q < NQX; ++q) {
         const int t = 4 * q + g;
-        vx[q] = (int)((int64_t)min(t, (int)p.M - 1) * p.lda * 2) + ((l16 ^ t) << 4);
+        vx[q] = (int)((int64_t)min(t, (int)p.M - 1) * p.lda * ES) + ((l16 ^ t) << 4);
     }
     uint8_t* my = lds + wave * S * STG;
     const int rot = n > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)n) : 0;
@@ -227,31 +258,32 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = mfma16<T>(wf[r][j], xf[j], acc[r]);
+            for (int r = 0; r < R; ++r) acc[r] = mfma_frag<T>(wf[r][j], xf[j], acc[r]);
         stage = stage + 1 == S ? 0 : stage + 1;
     }
 
     // partial last K step (zero-filled beyond K): the last wave, plain loads
-    if (wave == WAVES - 1 && (p.K & 127)) {
-        const int kb = nfull * 128;
+    if (wave == WAVES - 1 && (p.K % KS)) {
+        constexpr int FE = 16 / ES;                 // elements per 16-byte fragment unit
+        const int kb = nfull * KS;
         const bool xok = l16 < (int)p.M;
         const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
         u32x4 xt[4], wt[R][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int k = kb + j * 32 + g * 8;
+            const int k = kb + (4 * j + g) * FE;
             const int nvalid = (int)p.K - k;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = n0 + 16 * r + l16;
-                wt[r][j] = row < (int)p.N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, nvalid) : zero;
+                wt[r][j] = row < (int)p.N ? ld16_checked<T>(Wt + (int64_t)row * p.ldb + k, nvalid) : zero;
             }
-            xt[j] = xok ? ld8_checked(p.X + (int64_t)l16 * p.lda + k, nvalid) : zero;
+            xt[j] = xok ? ld16_checked<T>(Xt + (int64_t)l16 * p.lda + k, nvalid) : zero;
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < R; ++r) acc[r] = mfma16<T>(wt[r][j], xt[j], acc[r]);
+            for (int r = 0; r < R; ++r) acc[r] = mfma_frag<T>(wt[r][j], xt[j], acc[r]);
     }
 
     // the stages become the reduce buffer once every wave is done with them
@@ -308,6 +340,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
     constexpr int LP = P == 2 ? 1 : P == 4 ? 2 : P == 8 ? 3 : P == 16 ? 4 : P == 32 ? 5 : 6;
     static_assert((1 << LP) == P, "MM * RB must be a power of 2 in [2, 64]");
     __shared__ float red[4][P];
+    const uint16_t* pX = (const uint16_t*)p.X;
+    const uint16_t* pW = (const uint16_t*)p.W;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * RB;
     const int rows_here = min(RB, (int)p.N - n0);
@@ -315,10 +349,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
     // + K elements): rows past N, activation rows past M and k past K in the
     // last row read as zero and never touch memory beyond the allocation.
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(p.W + (int64_t)n0 * p.ldb), (short)0, (int)(((int64_t)(rows_here - 1) * p.ldb + p.K) * 2),
+        (void*)(pW + (int64_t)n0 * p.ldb), (short)0, (int)(((int64_t)(rows_here - 1) * p.ldb + p.K) * 2),
         0x00020000);
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)p.X, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + p.K) * 2), 0x00020000);
+        (void*)pX, (short)0, (int)(((int64_t)(p.M - 1) * p.lda + p.K) * 2), 0x00020000);
     const int nch = (int)((p.K + 511) / 512);
 
     float acc[MM][RB];
@@ -353,9 +387,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
         if (valid && nvalid < 8) {
 #pragma unroll
             for (int r = 0; r < RB; ++r)
-                ws[r] = r < rows_here ? ld8_checked(p.W + (int64_t)(n0 + r) * p.ldb + k, nvalid) : z;
+                ws[r] = r < rows_here ? ld16_checked(pW + (int64_t)(n0 + r) * p.ldb + k, nvalid) : z;
 #pragma unroll
-            for (int m = 0; m < MM; ++m) xs[m] = ld8_checked(p.X + (int64_t)m * p.lda + k, nvalid);
+            for (int m = 0; m < MM; ++m) xs[m] = ld16_checked(pX + (int64_t)m * p.lda + k, nvalid);
         }
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
@@ -469,6 +503,8 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
+    const uint16_t* pX = (const uint16_t*)p.X;
+    const uint16_t* pW = (const uint16_t*)p.W;
     const int wrow0 = blockIdx.x * WROWS + wave * 16 * R;     // this wave's first weight row
     const int nsteps = (K + 127) / 128, full_steps = K / 128;
     const int per = (nsteps + nsplit - 1) / nsplit;
@@ -487,8 +523,8 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
     // the read domain of the rows it copies
     const int wbase = min(wrow0, N - 1);
     const int wlast = min(wrow0 + 16 * R - 1, N - 1);
-    const i32x4 rw = rsrc_words(p.W + (int64_t)wbase * p.ldb, ((int64_t)(wlast - wbase) * p.ldb + K) * 2);
-    const i32x4 rx = rsrc_words(p.X, ((int64_t)(M - 1) * p.lda + K) * 2);
+    const i32x4 rw = rsrc_words(pW + (int64_t)wbase * p.ldb, ((int64_t)(wlast - wbase) * p.ldb + K) * 2);
+    const i32x4 rx = rsrc_words(pX, ((int64_t)(M - 1) * p.lda + K) * 2);
     int vw[4 * R], vx[MT];
 #pragma unroll
     for (int q = 0; q < 4 * R; ++q) {
@@ -568,12 +604,12 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = wrow0 + 16 * r + l16;
-                wt[r][j] = row < N ? ld8_checked(p.W + (int64_t)row * p.ldb + k, K - k) : zero;
+                wt[r][j] = row < N ? ld16_checked(pW + (int64_t)row * p.ldb + k, K - k) : zero;
             }
 #pragma unroll
             for (int t = 0; t < MT; ++t) {
                 const int xr = 16 * t + l16;
-                xt[t][j] = xr < M ? ld8_checked(p.X + (int64_t)xr * p.lda + k, K - k) : zero;
+                xt[t][j] = xr < M ? ld16_checked(pX + (int64_t)xr * p.lda + k, K - k) : zero;
             }
         }
 #pragma unroll
@@ -619,6 +655,138 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
         }
 }
 
+// ------------------------------------------------ fp32, W stored K x N
+// C[m][n] = alpha * sum_k X[m][k] * W[k][n] + ...,  M <= 16, each W row
+// N-contiguous: the reference's TB = 0 matvec (matvec_f32_tmpl.comp:27-58,
+// four contiguous columns per thread), here on the matrix cores.  One
+// v_mfma_f32_16x16x4_f32 takes 4 k of 16 activation rows (A operand: lane
+// (l16, g) holds X[l16][k]) against the same 4 k of 16 columns (B operand:
+// lane (l16, g) holds W[k][column of lane l16]).  A lane loads 16 bytes of a
+// W row, columns nl .. nl + 3 with nl = n0 + 4 l16, so each load instruction
+// reads 4 rows x 256 contiguous bytes (whole lines), and component c of the
+// loads feeds tile c, whose 16 columns are nl + c over the 16 lanes: four
+// accumulator tiles interleaved over the wave's 64 columns.  A 16-row chunk
+// is four MFMAs e per tile, MFMA e taking k = k0 + 4 g + e: lane group g loads
+// W rows k0 + 4 g .. + 3 and X[l16][k0 + 4 g .. + 3] (one 16-byte load).
+// Tile c's D[i][j] sits in lane (j, i / 4), component i % 4, so lane (l16, g)
+// owns C[4 g + r][nl .. nl + 3]: one 16-byte store per activation row.
+// Workgroup: 4 waves of 64 columns; grid.y splits the chunks into slices of
+// `per` chunks (PARTIAL: fp32 partials for the fixed-order reduce).  A
+// wave keeps U chunks of loads in flight while it multiplies the previous U.
+// Requires N % 4 == 0 (lanes past N load the last 4 columns and store
+// nothing), ldb % 4 == 0, lda % 4 == 0 (or M == 1) and 16-byte aligned X, W.
+// Activation rows past M load row M - 1 (their outputs are dropped); k past
+// K in the last chunk is zero in both operands.
+constexpr int SKN_COLS = 256;   // columns per workgroup
+
+template <typename TC, int U, bool PARTIAL>
+__global__ __launch_bounds__(256) void skinny_n_kernel(SkParams p, float* part, int per) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
+    const int nl = blockIdx.x * SKN_COLS + wave * 64 + 4 * l16;   // this lane's columns
+    const float* W = (const float*)p.W + min(nl, N - 4);
+    const float* X = (const float*)p.X + (int64_t)min(l16, M - 1) * p.lda;
+    const int64_t ldb = p.ldb;
+    const int chunks = (K + 15) / 16;
+    const int c_beg = (int)blockIdx.y * per;                       // per: chunks per slice
+    const int c_end = min(chunks, c_beg + per);
+    const int f_end = max(c_beg, min(c_end, K / 16));             // chunks with 16 valid k
+
+    floatx4 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int ch, floatx4 (&w)[U][4], floatx4 (&x)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t k = (int64_t)(ch + u) * 16 + 4 * g;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[u][e] = *(const floatx4*)(W + (k + e) * ldb);
+            x[u] = *(const floatx4*)(X + k);
+        }
+    };
+    auto mma = [&](const floatx4 (&w)[U][4], const floatx4 (&x)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u][e], w[u][e][c], acc[c], 0, 0, 0);
+    };
+    // full chunks in groups of U, the next group's loads in flight
+    const int ngrp = (f_end - c_beg) / U;
+    int ch = c_beg;
+    {
+        floatx4 wa[U][4], xa[U], wb[U][4], xb[U];
+        int i = 0;
+        if (ngrp > 0) load(ch, wa, xa);
+        for (; i + 1 < ngrp; i += 2) {
+            load(ch + U, wb, xb);
+            mma(wa, xa);
+            if (i + 2 < ngrp) load(ch + 2 * U, wa, xa);
+            mma(wb, xb);
+            ch += 2 * U;
+        }
+        if (i < ngrp) {
+            mma(wa, xa);
+            ch += U;
+        }
+    }
+    // the rest one chunk at a time, k past K zero
+    for (; ch < c_end; ++ch) {
+        const int k = ch * 16 + 4 * g;
+        floatx4 w[1][4], x[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool ok = k + e < K;
+            w[0][e] = ok ? *(const floatx4*)(W + (int64_t)(k + e) * ldb) : floatx4{0.f, 0.f, 0.f, 0.f};
+            x[0][e] = ok ? X[k + e] : 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0][e], w[0][e][c], acc[c], 0, 0, 0);
+    }
+
+    if (nl >= N) return;
+    if constexpr (PARTIAL) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m < M)
+                *(floatx4*)(part + ((int64_t)blockIdx.y * M + m) * N + nl) =
+                    floatx4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+        }
+    } else {
+        float alpha = p.alpha, beta = p.beta;
+        if (p.mode == 1) {
+            alpha = *(const float*)p.alpha_dev;
+            beta = *(const float*)p.beta_dev;
+        } else if (p.mode == 2) {
+            alpha = (float)*(const _Float16*)p.alpha_dev;
+            beta = (float)*(const _Float16*)p.beta_dev;
+        }
+        float b4[4] = {0.f, 0.f, 0.f, 0.f};
+        vkb::add_bias4(p.epi, nl, 4, b4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m >= M) continue;
+            TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
+            const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float y = alpha * acc[c][r];
+                if (beta != 0.0f) y += beta * (float)src[c];
+                if (p.epi.bias) y += b4[c];
+                dst[c] = (TC)y;
+            }
+        }
+    }
+}
+
 template <typename T, typename TC, int MM, int RB>
 int launch_gemv(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + RB - 1) / RB;
@@ -642,7 +810,7 @@ void launch_skl(const SkParams& p, hipStream_t st) {
     // least 512 workgroups (measured, n = 3-8: K=4096, O=14336 21.6 -> 19.5
     // us, K=4096, O=8192 12.3-12.8 -> 11.7 us; with 16 activation rows the
     // same split measured 0-4 % slower, so those keep four).
-    if (XR == 8 && p.K / 128 < 64 && grid >= 512) {
+    if (XR == 8 && p.K * sizeof(T) / 256 < 64 && grid >= 512) {
         hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, 2, R, 2>), dim3(grid), dim3(128), 0, st, p);
         return;
     }
@@ -651,7 +819,9 @@ void launch_skl(const SkParams& p, hipStream_t st) {
 
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
-    if (p.M <= 8)
+    if (sizeof(T) == 4 && p.M <= 4)
+        launch_skl<T, TC, 4, 1>(p, st);
+    else if (p.M <= 8)
         launch_skl<T, TC, 8, 1>(p, st);
     else if ((p.N + 31) / 32 >= 256)
         launch_skl<T, TC, 16, 2>(p, st);
@@ -706,31 +876,73 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
     return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
 }
 
+
+// skinny_n_kernel K split: slices of whole groups of 4 chunks (64 k), as
+// many as keep the grid to about two workgroups per CU, each slice at least
+// 8 groups long; SknPlan.per is the chunk count of a slice.
+struct SknPlan {
+    uint32_t split, per;
+};
+inline SknPlan skn_plan(uint32_t N, uint32_t K) {
+    const uint32_t wg = (N + SKN_COLS - 1) / SKN_COLS;
+    const uint32_t groups = (K + 63) / 64;
+    uint32_t sp = 512 / wg;
+    if (sp > groups / 8) sp = groups / 8;
+    if (sp > 64) sp = 64;
+    if (sp < 1) sp = 1;
+    const uint32_t gper = (groups + sp - 1) / sp;
+    return SknPlan{(groups + gper - 1) / gper, 4 * gper};
+}
+
+template <typename TC>
+int launch_skn(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) {
+    const SknPlan pl = skn_plan(p.N, p.K);
+    const dim3 grid((p.N + SKN_COLS - 1) / SKN_COLS, nsplit);
+    if (nsplit > 1)
+        hipLaunchKernelGGL((skinny_n_kernel<float, 2, true>), grid, dim3(256), 0, st, p, part, (int)pl.per);
+    else
+        hipLaunchKernelGGL((skinny_n_kernel<TC, 2, false>), grid, dim3(256), 0, st, p, part, (int)pl.per);
+    return (int)hipGetLastError();
+}
+
 }  // namespace
 
-extern "C" uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K) {
-    if ((int)M < DEC_MIN_M || M > 64) return 1;
+extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint32_t N, uint32_t K, int64_t lda,
+                                   int64_t ldb) {
+    if (M == 0 || N == 0 || K == 0 || lda <= 0 || ldb <= 0) return 0;
+    const int64_t es = ab_type == VKB_T_F32 ? 4 : 2;
+    const int64_t vec = 16 / es;
+    if ((M > 1 && (lda % vec || lda < (int64_t)K)) || ldb % vec) return 0;
+    if (ab_type == VKB_T_F32) {
+        if (M > 16) return 0;
+        if (!b_kmajor) return (N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(N, K).split;
+    } else if ((ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) || !b_kmajor || M > 64) {
+        return 0;
+    }
+    // the staged kernels address a 32-row weight tile and the activation
+    // rows (up to 16 ceil(M / 16) of them) with 32-bit buffer offsets: both
+    // spans must stay below 2 GiB
+    const uint64_t xrows = M <= 16 ? M : 16 * ((M + 15) / 16);
+    if (ldb < (int64_t)K || (uint64_t)32 * ldb * es >= (1ull << 31) ||
+        ((xrows - 1) * (uint64_t)lda + K) * es >= (1ull << 31))
+        return 0;
+    if (ab_type == VKB_T_F32 || (int)M < DEC_MIN_M) return 1;
     return dec_plan(N, K).split;
 }
 
-extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
+extern "C" int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64_t lda, const void* W, int64_t ldb,
                                  void* C, int64_t ldc, int c_type,
                                  uint32_t M, uint32_t N, uint32_t K,
                                  float alpha, float beta, int scalar_mode,
                                  const void* alpha_dev, const void* beta_dev,
                                  const vkb_epilogue_args* epi,
                                  float* part, uint32_t nsplit, void* stream) {
-    if (M == 0 || M > 64 || N == 0 || K == 0) return (int)hipErrorInvalidValue;
-    if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) return (int)hipErrorInvalidValue;
+    const uint32_t want = vkb_skinny_plan(ab_type, b_kmajor, M, N, K, lda, ldb);
+    if (want == 0 || nsplit != want || (nsplit > 1 && !part)) return (int)hipErrorInvalidValue;
     if (c_type != VKB_T_F32 && c_type != ab_type) return (int)hipErrorInvalidValue;
-    if ((lda & 7) || (ldb & 7) || ((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
-    if (nsplit != vkb_skinny_split(M, N, K) || (nsplit > 1 && !part)) return (int)hipErrorInvalidValue;
-    // buffer offsets are 32-bit: a 32-row weight tile and the activation
-    // tiles (rows up to 16 ceil(M / 16)) must span less than 2 GiB
-    const uint64_t xrows = M <= 16 ? M : 16 * ((M + 15) / 16);
-    if ((uint64_t)32 * ldb * 2 >= (1ull << 31) || xrows * lda * 2 >= (1ull << 31)) return (int)hipErrorInvalidValue;
+    if (((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
     SkParams p;
-    p.X = (const uint16_t*)X; p.W = (const uint16_t*)W; p.C = C;
+    p.X = X; p.W = W; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.M = M; p.N = N; p.K = K;
     p.alpha = alpha; p.beta = beta; p.mode = scalar_mode;
@@ -744,6 +956,10 @@ extern "C" int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const 
     p.epi.bias_type = epi ? epi->bias_type : 0;
     hipStream_t st = (hipStream_t)stream;
     const bool f32_out = c_type == VKB_T_F32;
+    if (ab_type == VKB_T_F32) {
+        if (!b_kmajor) return launch_skn<float>(p, part, nsplit, st);
+        return launch_sk_lds<float, float>(p, st);
+    }
     return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, part, (int)nsplit, st)
                                  : launch_typed<_Float16>(p, f32_out, part, (int)nsplit, st);
 }

@@ -109,15 +109,21 @@ int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, uint32_t spli
                              const void* alpha_dev, const void* beta_dev,
                              const vkb_epilogue_args* epi, void* stream);
 
-/* Skinny 16-bit GEMM for decode (M <= 64 rows of activations):
- *   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n]
- * X = A (K-contiguous rows, lda), W = B (K-contiguous rows, ldb); ab_type F16
- * or BF16, c_type F32 or ab_type.  Requires lda, ldb multiples of 8 and
- * 16-byte aligned A, B.  nsplit must be vkb_skinny_split(M, N, K); when it
- * is > 1 the kernel writes fp32 partials to part ([nsplit][M][N], row pitch
+/* Skinny GEMM for decode (a few activation rows X against a weight W):
+ *   C[m][n] = alpha * sum_k X[m][k] * W'[k][n] + beta * C_in[m][n] + bias[n]
+ * X = A (K-contiguous rows, lda).  b_kmajor = 1: W = B stored N x K
+ * (W'[k][n] = B[n*ldb + k]); b_kmajor = 0: W = B stored K x N
+ * (B[k*ldb + n]).  Kernels exist for
+ *   fp16 / bf16, b_kmajor, M <= 64, c_type F32 or ab_type;
+ *   fp32, either layout, M <= 16, c_type F32 (b_kmajor = 0 needs N % 4 == 0).
+ * lda (unless M == 1) and ldb must be multiples of 16 bytes of elements,
+ * A and B 16-byte aligned.  vkb_skinny_plan returns the K split the launch
+ * must be given (0: no skinny kernel for these arguments); with a split
+ * above 1 the kernel writes fp32 partials to part ([split][M][N], row pitch
  * N) and the caller finishes with vkb_launch_splitk_reduce. */
-uint32_t vkb_skinny_split(uint32_t M, uint32_t N, uint32_t K);
-int vkb_launch_skinny(int ab_type, const void* X, int64_t lda, const void* W, int64_t ldb,
+uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint32_t N, uint32_t K, int64_t lda,
+                         int64_t ldb);
+int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64_t lda, const void* W, int64_t ldb,
                       void* C, int64_t ldc, int c_type,
                       uint32_t M, uint32_t N, uint32_t K,
                       float alpha, float beta, int scalar_mode,
