@@ -200,17 +200,17 @@ def test_plan_decode_split():
 def test_plan_skinny_f32():
     """fp32 with up to 16 activation rows (op_a = N, fp32 output): the skinny
     kernels for W stored N x K (op_b = T, no split) and K x N (op_b = N, N a
-    multiple of 4, K split in whole 64-row groups so that the grid holds
-    about 512 workgroups of 256 columns, each slice at least 8 groups)."""
+    multiple of 4, K split in whole 64-row groups so that the grid holds at
+    most 256 workgroups of 128 columns, each slice at least 4 groups)."""
     for M in (1, 2, 4, 9, 16):
         for ob in (0, 1):
             pl = P(vk.DT_F32, vk.DT_F32, 0, ob, M, 8192, 8192, 8192, 8192, 8192)
             assert pl.path == vk.PATH_SKINNY
-            assert pl.split == (1 if ob else 16)     # 32 column blocks x 16 slices
-    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 16, 4096, 14336, 14336, 4096, 4096).split == 28
-    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 14336, 4096, 4096, 14336, 14336).split == 8
-    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 1024, 65536, 65536, 1024, 1024).split == 64
-    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 3, 8192, 1000, 1000, 8192, 8192).split == 2
+            assert pl.split == (1 if ob else 4)      # 64 column blocks x 4 slices
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 16, 4096, 14336, 14336, 4096, 4096).split == 8
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 14336, 4096, 4096, 14336, 14336).split == 2
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 1024, 65536, 65536, 1024, 1024).split == 32
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 3, 8192, 1000, 1000, 8192, 8192).split == 4
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 4, 1, 4, 4, 4).split == 1
     # not skinny: 17 rows, 16-bit output, N % 4 (K x N), op_a = T, misaligned
     # leading dimensions, ldb short of N

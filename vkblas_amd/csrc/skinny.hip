@@ -663,91 +663,108 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 // (l16, g) holds X[l16][k]) against the same 4 k of 16 columns (B operand:
 // lane (l16, g) holds W[k][column of lane l16]).  A lane loads 16 bytes of a
 // W row, columns nl .. nl + 3 with nl = n0 + 4 l16, so each load instruction
-// reads 4 rows x 256 contiguous bytes (whole lines), and component c of the
-// loads feeds tile c, whose 16 columns are nl + c over the 16 lanes: four
-// accumulator tiles interleaved over the wave's 64 columns.  A 16-row chunk
-// is four MFMAs e per tile, MFMA e taking k = k0 + 4 g + e: lane group g loads
-// W rows k0 + 4 g .. + 3 and X[l16][k0 + 4 g .. + 3] (one 16-byte load).
-// Tile c's D[i][j] sits in lane (j, i / 4), component i % 4, so lane (l16, g)
-// owns C[4 g + r][nl .. nl + 3]: one 16-byte store per activation row.
-// Workgroup: 4 waves of 64 columns; grid.y splits the chunks into slices of
-// `per` chunks (PARTIAL: fp32 partials for the fixed-order reduce).  A
-// wave keeps U chunks of loads in flight while it multiplies the previous U.
+// reads 4 rows x 256 contiguous bytes (whole lines, non-temporal: the weights
+// stream through once), and component c of the loads feeds tile c, whose 16
+// columns are nl + c over the 16 lanes: four accumulator tiles interleaved
+// over the wave's 64 columns.  A 16-row chunk is four MFMAs e per tile, MFMA
+// e taking k = k0 + 4 g + e: lane group g loads W rows k0 + 4 g .. + 3 and
+// X[l16][k0 + 4 g .. + 3] (one 16-byte load).  Tile c's D[i][j] sits in lane
+// (j, i / 4), component i % 4, so lane (l16, g) owns C[4 g + r][nl .. nl + 3]:
+// one 16-byte store per activation row.
+// Workgroup: WV waves, WV / KW column groups of 64 side by side, KW waves
+// along K splitting the workgroup's slice into contiguous parts whose sums
+// are added in LDS in wave order.  Each wave loads the next chunk while it
+// multiplies the current one.  grid.y splits K into slices of `per` chunks
+// (PARTIAL: fp32 partials for the fixed-order reduce); the plan keeps the
+// grid to one round of at most 256 workgroups, one per CU (measured on
+// 8192x8192, 4096x14336 and 14336x4096: 0.74-0.82 of HBM; 384-512
+// workgroups, two per CU, 0.58-0.71).
 // Requires N % 4 == 0 (lanes past N load the last 4 columns and store
 // nothing), ldb % 4 == 0, lda % 4 == 0 (or M == 1) and 16-byte aligned X, W.
 // Activation rows past M load row M - 1 (their outputs are dropped); k past
 // K in the last chunk is zero in both operands.
-constexpr int SKN_COLS = 256;   // columns per workgroup
+constexpr int SKN_WV = 8, SKN_KW = 4;
+constexpr int SKN_COLS = 64 * SKN_WV / SKN_KW;   // columns per workgroup
 
-template <typename TC, int U, bool PARTIAL>
-__global__ __launch_bounds__(256) void skinny_n_kernel(SkParams p, float* part, int per) {
+template <typename TC, int WV, int KW, bool PARTIAL>
+__global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* part, int per) {
+    constexpr int CG = WV / KW;                  // column groups of 64 per workgroup
+    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * 4 * 64 : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cg = wave % CG, kw = wave / CG;
     const int l16 = lane & 15, g = lane >> 4;
     const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
-    const int nl = blockIdx.x * SKN_COLS + wave * 64 + 4 * l16;   // this lane's columns
+    const int nl = blockIdx.x * (64 * CG) + cg * 64 + 4 * l16;   // this lane's columns
     const float* W = (const float*)p.W + min(nl, N - 4);
     const float* X = (const float*)p.X + (int64_t)min(l16, M - 1) * p.lda;
     const int64_t ldb = p.ldb;
     const int chunks = (K + 15) / 16;
-    const int c_beg = (int)blockIdx.y * per;                       // per: chunks per slice
-    const int c_end = min(chunks, c_beg + per);
+    const int s_beg = (int)blockIdx.y * per;                      // the workgroup's slice
+    const int s_end = min(chunks, s_beg + per);
+    const int sub = (per + KW - 1) / KW;                          // this wave's part of it
+    const int c_beg = min(s_end, s_beg + kw * sub);
+    const int c_end = min(s_end, c_beg + sub);
     const int f_end = max(c_beg, min(c_end, K / 16));             // chunks with 16 valid k
 
     floatx4 acc[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto load = [&](int ch, floatx4 (&w)[U][4], floatx4 (&x)[U]) {
+    auto load = [&](int ch, floatx4 (&w)[4], floatx4& x) {
+        const int64_t k = (int64_t)ch * 16 + 4 * g;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t k = (int64_t)(ch + u) * 16 + 4 * g;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) w[u][e] = *(const floatx4*)(W + (k + e) * ldb);
-            x[u] = *(const floatx4*)(X + k);
-        }
+        for (int e = 0; e < 4; ++e) w[e] = __builtin_nontemporal_load((const floatx4*)(W + (k + e) * ldb));
+        x = *(const floatx4*)(X + k);
     };
-    auto mma = [&](const floatx4 (&w)[U][4], const floatx4 (&x)[U]) {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[u][e], w[u][e][c], acc[c], 0, 0, 0);
-    };
-    // full chunks in groups of U, the next group's loads in flight
-    const int ngrp = (f_end - c_beg) / U;
-    int ch = c_beg;
-    {
-        floatx4 wa[U][4], xa[U], wb[U][4], xb[U];
-        int i = 0;
-        if (ngrp > 0) load(ch, wa, xa);
-        for (; i + 1 < ngrp; i += 2) {
-            load(ch + U, wb, xb);
-            mma(wa, xa);
-            if (i + 2 < ngrp) load(ch + 2 * U, wa, xa);
-            mma(wb, xb);
-            ch += 2 * U;
-        }
-        if (i < ngrp) {
-            mma(wa, xa);
-            ch += U;
-        }
-    }
-    // the rest one chunk at a time, k past K zero
-    for (; ch < c_end; ++ch) {
-        const int k = ch * 16 + 4 * g;
-        floatx4 w[1][4], x[1];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const bool ok = k + e < K;
-            w[0][e] = ok ? *(const floatx4*)(W + (int64_t)(k + e) * ldb) : floatx4{0.f, 0.f, 0.f, 0.f};
-            x[0][e] = ok ? X[k + e] : 0.f;
-        }
+    auto mma = [&](const floatx4 (&w)[4], const floatx4& x) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-                acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[0][e], w[0][e][c], acc[c], 0, 0, 0);
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e][c], acc[c], 0, 0, 0);
+    };
+    // full chunks, the next chunk's loads in flight
+    const int nf = f_end - c_beg;
+    int ch = c_beg;
+    {
+        floatx4 wa[4], xa, wb[4], xb;
+        int i = 0;
+        if (nf > 0) load(ch, wa, xa);
+        for (; i + 1 < nf; i += 2) {
+            load(ch + 1, wb, xb);
+            mma(wa, xa);
+            if (i + 2 < nf) load(ch + 2, wa, xa);
+            mma(wb, xb);
+            ch += 2;
+        }
+        if (i < nf) {
+            mma(wa, xa);
+            ++ch;
+        }
+    }
+    // the partial last chunk, k past K zero
+    for (; ch < c_end; ++ch) {
+        const int k = ch * 16 + 4 * g;
+        floatx4 w[4], x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const bool ok = k + e < K;
+            w[e] = ok ? *(const floatx4*)(W + (int64_t)(k + e) * ldb) : floatx4{0.f, 0.f, 0.f, 0.f};
+            x[e] = ok ? X[k + e] : 0.f;
+        }
+        mma(w, x);
+    }
+    // the KW parts of the slice, summed in wave order
+    if constexpr (KW > 1) {
+        if (kw > 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) red[(((kw - 1) * CG + cg) * 4 + c) * 64 + lane] = acc[c];
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int j = 1; j < KW; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] += red[(((j - 1) * CG + cg) * 4 + c) * 64 + lane];
     }
 
     if (nl >= N) return;
@@ -876,18 +893,17 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
     return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
 }
 
-
 // skinny_n_kernel K split: slices of whole groups of 4 chunks (64 k), as
-// many as keep the grid to about two workgroups per CU, each slice at least
-// 8 groups long; SknPlan.per is the chunk count of a slice.
+// many as keep the grid within 256 workgroups, each slice at least 4
+// groups long; SknPlan.per is the chunk count of a slice.
 struct SknPlan {
     uint32_t split, per;
 };
 inline SknPlan skn_plan(uint32_t N, uint32_t K) {
     const uint32_t wg = (N + SKN_COLS - 1) / SKN_COLS;
     const uint32_t groups = (K + 63) / 64;
-    uint32_t sp = 512 / wg;
-    if (sp > groups / 8) sp = groups / 8;
+    uint32_t sp = 256 / wg;
+    if (sp > groups / 4) sp = groups / 4;
     if (sp > 64) sp = 64;
     if (sp < 1) sp = 1;
     const uint32_t gper = (groups + sp - 1) / sp;
@@ -897,11 +913,11 @@ inline SknPlan skn_plan(uint32_t N, uint32_t K) {
 template <typename TC>
 int launch_skn(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) {
     const SknPlan pl = skn_plan(p.N, p.K);
-    const dim3 grid((p.N + SKN_COLS - 1) / SKN_COLS, nsplit);
+    const dim3 grid((p.N + SKN_COLS - 1) / SKN_COLS, nsplit), block(64 * SKN_WV);
     if (nsplit > 1)
-        hipLaunchKernelGGL((skinny_n_kernel<float, 2, true>), grid, dim3(256), 0, st, p, part, (int)pl.per);
+        hipLaunchKernelGGL((skinny_n_kernel<float, SKN_WV, SKN_KW, true>), grid, block, 0, st, p, part, (int)pl.per);
     else
-        hipLaunchKernelGGL((skinny_n_kernel<TC, 2, false>), grid, dim3(256), 0, st, p, part, (int)pl.per);
+        hipLaunchKernelGGL((skinny_n_kernel<TC, SKN_WV, SKN_KW, false>), grid, block, 0, st, p, part, (int)pl.per);
     return (int)hipGetLastError();
 }
 
