@@ -147,7 +147,7 @@ def test_sgemm_engine_success_does_not_forward(layer):
 
 @pytest.mark.parametrize("status", [1, 2, 3])
 def test_every_engine_error_forwards(layer, status):
-    """VKBLAS_ERR_PARAM / ERR_INIT / ERR_DEVICE alike: the vendor computes."""
+    """VKBLAS_ERR_INIT / ERR_IMPORT / ERR_PARAM alike: the vendor computes."""
     run_case(layer, """
         st = L.hipblasSgemmStridedBatched(h, T, N, 8, 8, 8, ctypes.byref(alpha), A, 8, ctypes.c_longlong(64), B, 8,
                                           ctypes.c_longlong(64), ctypes.byref(beta), C, 8, ctypes.c_longlong(64), 3)
