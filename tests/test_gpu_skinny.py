@@ -64,12 +64,20 @@ CASES += [
     (16, 8192, 520, 0, 0, 0.5, "bf16"),
     (9, 8216, 1001, 7, 15, -0.5, "f16>f32"),
 ]
+# 9-16 activation rows with a longer K on two weight tiles, two waves and
+# three stages per wave
+CASES += [
+    (13, 8300, 6000, 8, 0, 0.5, "f16>f32"),
+]
 # up to 8 activation rows, at least 512 workgroups and fewer than 64 K steps:
-# two waves per workgroup (ragged K tail on the second wave; a single step)
+# two waves per workgroup (ragged K tail on the second wave; a single step);
+# with 24-40 K steps and 32-row workgroups spreading as evenly as 16-row
+# ones, two weight tiles and three stages (the 4104 and 4100 cases)
 CASES += [
     (5, 8200, 1032, 8, 8, 0.0, "f16"),
     (8, 8192, 4104, 0, 8, 0.5, "bf16"),
     (3, 8192, 136, 8, 8, -0.5, "f16>f32"),
+    (6, 14400, 4100, 4, 12, 0.0, "f16"),
 ]
 # 17-64 activation rows on both decode geometries: R = 2 (128 weight rows per
 # workgroup, when its grid fills >= 240 CUs: K split 4, then no split with a
@@ -160,9 +168,10 @@ def test_decode_deterministic():
     from gpu_helpers import to_dev, to_host
     print("[case] decode determinism", flush=True)
     # every kernel and geometry: GEMV, staged skinny with one and two weight
-    # tiles per workgroup, staged decode with 64 and 128 weight rows
-    for M, N, K in ((1, 2048, 4096), (3, 2048, 4096), (9, 2048, 4096), (16, 8192, 1024), (40, 2048, 4096),
-                    (64, 8192, 2048)):
+    # tiles per workgroup (two tiles for 9-16 and for up to 8 rows), staged
+    # decode with 64 and 128 weight rows
+    for M, N, K in ((1, 2048, 4096), (3, 2048, 4096), (9, 2048, 4096), (16, 8192, 1024), (8, 8192, 4096),
+                    (40, 2048, 4096), (64, 8192, 2048)):
         dX, dW = to_dev(_padded(M, K, K, 21, 1.0)), to_dev(_padded(N, K, K, 22, 0.05))
         outs = []
         for _ in range(3):

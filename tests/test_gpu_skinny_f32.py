@@ -39,6 +39,7 @@ CASES_T += [
     (8, 8192, 1000, 0, 4, 0, 0.0),       # 512 workgroups, 16 K steps: two waves each
     (12, 8200, 1032, 4, 4, 3, 0.25),     # two weight tiles per workgroup, ragged last one
     (16, 8192, 520, 0, 0, 0, 0.5),
+    (10, 8240, 3000, 4, 0, 0, 0.5),      # two tiles, two waves, three stages over 46 K steps
     (16, 64, 13, 3, 3, 2, -0.5),
 ]
 

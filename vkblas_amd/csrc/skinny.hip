@@ -811,39 +811,64 @@ int launch_gemv(const SkParams& p, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
-// Staged skinny: XR activation rows staged per step (8 or 16, covering M),
-// two stages per wave.  Up to 8 rows XR = 8 (measured against XR = 4 for
-// 3-4 rows: 8192x8192 22.0 -> 21.4 us, 4096x14336 21.6 -> 21.9 us).  From 9
-// activation rows the activation copies weigh as much as the weight copies;
-// two weight tiles per workgroup share them when that still leaves one round
-// of at least 256 workgroups (measured: 8192x8192 n = 16 23.5 -> 22.3 us,
-// K=4096, O=14336 24.0 -> 22.0 us; with 128 workgroups, K=14336, O=4096,
-// 22.2 -> 29.3 us).
-template <typename T, typename TC, int XR, int R>
+// Staged skinny geometry: XR activation rows staged per step (4 for fp32 up
+// to 4 rows, else 8 or 16, covering M); R 16-row weight tiles and WAVES waves
+// per workgroup; S LDS stages per wave.
+//  * 9-16 rows, and a grid of 32-row workgroups that fills the chip (at least
+//    256): R = 2 (two tiles share every activation copy, which from 9 rows
+//    weigh as much as the weight copies), two waves (each a K half), three
+//    stages.  Measured (fp16, us) against R = 2 with four waves and two
+//    stages: K=4096, O=14336 n = 12 / 16 21.1 / 21.9 -> 19.5 / 19.9;
+//    K=8192, O=8192 n = 16 22.3 -> 21.9; K=2048, O=16384 14.1 -> 13.0;
+//    K=4096, O=11008 20.5 -> 18.5; K=8192, O=28672 80.1 -> 77.6; fp32
+//    K=4096, O=14336 42.0 -> 39.1.
+//  * up to 8 rows of 16-bit types with 24-40 K steps, when 32-row workgroups
+//    fill the chip no less evenly than 16-row ones (the busiest CU gets no
+//    more rows): the same R = 2, two-wave, three-stage form.  K=4096,
+//    O=14336 n = 3-8 20.6-21.1 -> 18.7-19.1 us; K=4096, O=8192 12.0-12.5 ->
+//    11.8-12.3.  Not where R = 2 spreads worse (K=4096, O=11008: 16.5 ->
+//    18.8), nor with 16 K steps (K=2048, O=16384: 11.6 -> 12.5) or with 64
+//    (K=8192, O=8192: 21.0 -> 22.0), nor for fp32 (K=2048, O=16384 n = 8:
+//    21.2 -> 23.0).
+//  * otherwise one tile, two stages; up to 8 rows two waves per workgroup
+//    (each a K half) when four would leave each wave fewer than 16 K steps
+//    and the grid has at least 512 workgroups (measured, n = 3-8: K=4096,
+//    O=14336 21.6 -> 19.5 us, K=4096, O=8192 12.3-12.8 -> 11.7 us), else
+//    four waves.
+struct SklPlan {
+    int xr, r, waves, stages;
+};
+inline SklPlan skl_plan(uint32_t es, uint32_t M, uint32_t N, uint32_t K) {
+    const int xr = (es == 4 && M <= 4) ? 4 : M <= 8 ? 8 : 16;
+    const uint32_t ksteps = K * es / 256;
+    const uint32_t g16 = (N + 15) / 16, g32 = (N + 31) / 32;
+    if (xr == 16) return g32 >= 256 ? SklPlan{16, 2, 2, 3} : SklPlan{16, 1, 4, 2};
+    if (xr == 8 && es == 2 && ksteps >= 24 && ksteps <= 40 && g32 >= 256 &&
+        2 * ((g32 + 255) / 256) <= (g16 + 255) / 256)
+        return SklPlan{8, 2, 2, 3};
+    if (xr == 8 && ksteps < 64 && g16 >= 512) return SklPlan{8, 1, 2, 2};
+    return SklPlan{xr, 1, 4, 2};
+}
+
+template <typename T, typename TC, int XR, int S, int R, int WAVES>
 void launch_skl(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + 16 * R - 1) / (16 * R);
-    // Up to 8 activation rows: two waves per workgroup (each a K half) when
-    // four would leave each wave fewer than 16 K steps and the grid has at
-    // least 512 workgroups (measured, n = 3-8: K=4096, O=14336 21.6 -> 19.5
-    // us, K=4096, O=8192 12.3-12.8 -> 11.7 us; with 16 activation rows the
-    // same split measured 0-4 % slower, so those keep four).
-    if (XR == 8 && p.K * sizeof(T) / 256 < 64 && grid >= 512) {
-        hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, 2, R, 2>), dim3(grid), dim3(128), 0, st, p);
-        return;
-    }
-    hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, 2, R, 4>), dim3(grid), dim3(256), 0, st, p);
+    hipLaunchKernelGGL((skinny_lds_kernel<T, TC, XR, S, R, WAVES>), dim3(grid), dim3(64 * WAVES), 0, st, p);
 }
 
 template <typename T, typename TC>
 int launch_sk_lds(const SkParams& p, hipStream_t st) {
-    if (sizeof(T) == 4 && p.M <= 4)
-        launch_skl<T, TC, 4, 1>(p, st);
-    else if (p.M <= 8)
-        launch_skl<T, TC, 8, 1>(p, st);
-    else if ((p.N + 31) / 32 >= 256)
-        launch_skl<T, TC, 16, 2>(p, st);
-    else
-        launch_skl<T, TC, 16, 1>(p, st);
+    const SklPlan g = skl_plan(sizeof(T), p.M, p.N, p.K);
+    if (g.xr == 16) {
+        if (g.r == 2) launch_skl<T, TC, 16, 3, 2, 2>(p, st);
+        else launch_skl<T, TC, 16, 2, 1, 4>(p, st);
+    } else if (g.xr == 8) {
+        if (g.r == 2) launch_skl<T, TC, 8, 3, 2, 2>(p, st);
+        else if (g.waves == 2) launch_skl<T, TC, 8, 2, 1, 2>(p, st);
+        else launch_skl<T, TC, 8, 2, 1, 4>(p, st);
+    } else {
+        if constexpr (sizeof(T) == 4) launch_skl<T, TC, 4, 2, 1, 4>(p, st);
+    }
     return (int)hipGetLastError();
 }
 
