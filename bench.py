@@ -384,7 +384,7 @@ def main():
     log("[bench] fp32 matvec 8192x8192, both weight layouts")
     line["fp32_matvec_8192"] = matvec_f32(torch, vk, stream, args.steps)
     log("[bench] split-K and strided-batched")
-    line["splitk_256x256"] = splitk(torch, vk, stream, args.steps, splits=(0,))
+    line["splitk_256x256"] = splitk(torch, vk, stream, args.steps)
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
     if not args.no_cpu:
         # last, so the GPU legs run back to back without an idle gap between them
