@@ -13,7 +13,7 @@ copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--only fp32|fp16|bf16|matvec|bf16mv|f32mv|splitk|batched|ceiling|vendor]
+                  [--only fp32|fp16|bf16|matvec|matvec_ns|bf16mv|f32mv|splitk|batched|ceiling|vendor]
 """
 import argparse
 import json
@@ -281,7 +281,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "bf16mv", "f32mv", "splitk", "batched",
+    ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "matvec_ns", "bf16mv", "f32mv", "splitk", "batched",
                                        "calibrate", "ceiling", "vendor"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
@@ -305,6 +305,10 @@ def main():
     if args.only == "matvec":
         print(json.dumps({"n1-16": matvec(torch, vk, stream, args.steps),
                           "n24-64": matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))}))
+        return
+    if args.only == "matvec_ns":
+        print(json.dumps({"4096x14336": matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 4, 8, 12, 16)),
+                          "14336x4096": matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 4, 8, 12, 16))}))
         return
     if args.only == "bf16mv":
         print(json.dumps(matvec(torch, vk, stream, args.steps, bf16=True)))
