@@ -64,6 +64,26 @@ class Timer:
         return [s.elapsed_time(e) for s, e in self.pairs]
 
 
+WARM_MS = 20.0
+
+
+def warm(torch, fn, ms=WARM_MS):
+    """Untimed launches fn(i), ten at a time, until `ms` of wall time have
+    passed: from a cold start (fresh buffers, the GPU idle during host work)
+    the first milliseconds of a leg ran up to 15 % slower than the steady
+    state (fp16 4096^3: 109-116 against 100 us), which three warmup launches
+    did not cover."""
+    i = 0
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= ms:
+            return i
+
+
 def batch_ms(torch, stream, fn, launches, batches=5):
     """Median over `batches` of the average launch duration of `launches`
     back-to-back calls fn(i) between one pair of HIP events on `stream` (a
@@ -151,8 +171,7 @@ def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
         def call():
             vk.gemm_async(vdt, cdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
                           C.data_ptr(), n, stream=sp)
-        for _ in range(3):
-            call()
+        warm(torch, lambda i: call())
         med = batch_ms(torch, stream, lambda i: call(), max(steps, 20))
         out[name] = {"ms": round(med, 4), "tflops": round(2.0 * n ** 3 / (med * 1e-3) / 1e12, 1),
                      "path": vk.PATH_NAMES[vk.last_path()]}
@@ -176,8 +195,7 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
         def call(i):
             vk.gemm_async(vdt, vdt, vk.OP_N, vk.OP_T, nt, O, K, 1.0, X.data_ptr(), K,
                           Ws[i % 3].data_ptr(), K, 0.0, Y.data_ptr(), O, stream=sp)
-        for i in range(6):
-            call(i)
+        warm(torch, call)
         med = batch_ms(torch, stream, call, 3 * max(steps, 10))
         nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
         gbs = nbytes / (med * 1e-3) / 1e9
@@ -203,8 +221,7 @@ def matvec_f32(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16)):
             def call(i):
                 vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, ob, nt, O, K, 1.0, X.data_ptr(), K,
                               Ws[i % 3].data_ptr(), ldw, 0.0, Y.data_ptr(), O, stream=sp)
-            for i in range(6):
-                call(i)
+            warm(torch, call)
             med = batch_ms(torch, stream, call, 3 * max(steps, 10))
             nbytes = 4 * O * K + 4 * K * nt + 4 * O * nt
             gbs = nbytes / (med * 1e-3) / 1e9
@@ -235,8 +252,7 @@ def mfma_ceiling(torch, vk, stream, steps):
 
             def call(i):
                 probe.mfma_probe(bf16, ops.data_ptr(), out.data_ptr(), blocks, iters, stream=sp)
-            for i in range(3):
-                call(i)
+            warm(torch, call)
             med = batch_ms(torch, stream, call, max(steps, 20))
             tf = flops / (med * 1e-3) / 1e12
             res[f"{name}_{data}"] = {"tflops": round(tf, 1), "frac_of_peak": round(tf / PEAK_FP16_TFLOPS, 4)}
@@ -430,8 +446,7 @@ def splitk(torch, vk, stream, steps, splits=(4, 16, 64, 0)):
                     vk.gemm_async(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, 1.0,
                                   A.data_ptr(), K, B.data_ptr(), 256, 0.0, C.data_ptr(), 256, split_k=split,
                                   stream=sp)
-                for _ in range(3):
-                    call()
+                warm(torch, lambda i: call())
                 med = batch_ms(torch, stream, lambda i: call(), max(steps, 10))
                 tf = 2.0 * 256 * 256 * K / (med * 1e-3) / 1e12
                 gbs = (A.numel() + B.numel()) * A.element_size() / (med * 1e-3) / 1e9
@@ -461,8 +476,7 @@ def vendor(torch, vk, stream, steps):
         b = (torch.randn(n, n, device="cuda:0", generator=g) / math.sqrt(n)).to(dt)
         bt = b.t().contiguous()
         for lay, f in (("NN", lambda: a @ b), ("TN", lambda: a @ bt.t())):
-            for _ in range(3):
-                f()
+            warm(torch, lambda i: f())
             med = batch_ms(torch, stream, lambda i: f(), max(steps, 20))
             out[f"{name}_{n}_{lay}"] = {"ms": round(med, 4), "tflops": round(2.0 * n ** 3 / (med * 1e-3) / 1e12, 1)}
     K = O = 8192
@@ -470,8 +484,7 @@ def vendor(torch, vk, stream, steps):
     X = torch.randn(64, K, device="cuda:0", generator=g).half()
     for nt in (1, 4, 8, 16, 24, 32, 64):
         x = X[:nt]
-        for i in range(6):
-            x @ Ws[i % 3].t()
+        warm(torch, lambda i: x @ Ws[i % 3].t())
         med = batch_ms(torch, stream, lambda i: x @ Ws[i % 3].t(), 3 * max(steps, 10))
         nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
         out[f"decode_8192_n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
@@ -490,8 +503,7 @@ def batched(torch, vk, stream, steps):
     def call():
         vk.gemm_async(vk.DT_F32, vk.DT_F32, 0, 0, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0, C.data_ptr(),
                       n, nb, n * n, n * n, n * n, stream=sp)
-    for _ in range(3):
-        call()
+    warm(torch, lambda i: call())
     med = batch_ms(torch, stream, lambda i: call(), max(steps, 20))
     tf = 2.0 * nb * n ** 3 / (med * 1e-3) / 1e12
     return {"ms": round(med, 4), "tflops": round(tf, 2), "frac_of_peak": round(tf / PEAK_FP32_TFLOPS, 4),
