@@ -261,14 +261,18 @@ def test_plan_forced_split(K, split, dt):
     assert pl.k_per_split % bk == 0
     assert pl.split * pl.k_per_split >= K > (pl.split - 1) * pl.k_per_split
     assert pl.split == split
+    # 64 slices of the four 128x128 tiles fill the CUs: the pipelined
+    # 128x128 kernel; fewer slices keep the 64x64 tiles
+    assert pl.tile == (1 if split == 64 else 0)
 
 
 def test_plan_split_heuristic_and_off():
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and 2 <= pl.split <= 256
-    # whole 256x256 tiles: pass 1 on the pipelined kernel, slices of whole K-step pairs
-    assert pl.tile == 2 and pl.k_per_split % 64 == 0
-    # 16-bit inputs: 128x128 tiles, about a workgroup per CU
+    # whole 128x128 tiles: pass 1 on the pipelined kernel, slices of whole
+    # K-step pairs, about a workgroup per CU
+    assert pl.tile == 1 and pl.k_per_split % 64 == 0 and 4 * pl.split <= 256
+    # 16-bit inputs: the same
     pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 262144, 262144, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 128 == 0 and 4 * pl.split <= 256
     # ragged M: the 128x128 generic split

@@ -227,14 +227,14 @@ def test_splitk(K, dtype, split):
 
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
-@pytest.mark.parametrize("mode", ["auto", "ragged"])
+@pytest.mark.parametrize("mode", ["auto", "ragged", "ragged128"])
 def test_splitk_pipelined(dtype, op_a, op_b, mode):
     """Split-K pass 1 on the pipelined kernel, every layout.  auto: the
-    planner's choice at M = N = 256, K = 16384 (256x256 tiles for fp32,
-    128x128 four-stage tiles for 16-bit inputs; alpha = 1, beta = 0, 16-bit
-    output for 16-bit inputs); ragged: tile forced to 256, a 256 x 512
-    output, split 7 over K = 8448 (the last slice shorter), alpha / beta on an
-    fp32 C.  Bitwise reproducible run to run."""
+    planner's choice at M = N = 256, K = 16384 (128x128 tiles: two-stage for
+    fp32, four-stage for 16-bit inputs; alpha = 1, beta = 0, 16-bit output
+    for 16-bit inputs); ragged / ragged128: tile forced to 256 / 128, a
+    256 x 512 output, split 7 over K = 8448 (the last slice shorter), alpha /
+    beta on an fp32 C.  Bitwise reproducible run to run."""
     import vkblas_amd as vk
     from gpu_helpers import to_dev, to_host, normwise, f32_bound, F16_BOUND, BF16_BOUND
     auto = mode == "auto"
@@ -253,11 +253,11 @@ def test_splitk_pipelined(dtype, op_a, op_b, mode):
     ct = dt if out16 else vk.DT_F32
     hC = conv(c) if out16 else c
     if not auto:
-        vk.set_override(2, False)
+        vk.set_override(1 if mode == "ragged128" else 2, False)
     try:
         pl = vk.plan(dt, ct, op_a, op_b, M, N, K, lda, ldb, N, split_k=0 if auto else 7)
-        # the planner: 256x256 tiles for fp32, 128x128 (four-stage pass 1) for 16-bit inputs
-        tile = 1 if (auto and dtype != "f32") else 2
+        # the planner: 128x128 tiles
+        tile = 2 if mode == "ragged" else 1
         assert pl.path == vk.PATH_SPLITK and pl.tile == tile
         step2 = 64 if dtype == "f32" else 128
         assert pl.k_per_split % step2 == 0 and (K - (pl.split - 1) * pl.k_per_split) % step2 == 0
@@ -273,6 +273,10 @@ def test_splitk_pipelined(dtype, op_a, op_b, mode):
             vk.gemm_async(dt, ct, op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb, beta,
                           dC.data_ptr(), N, split_k=0 if auto else 7)
             assert vk.last_path() == vk.PATH_SPLITK
+            # pipelined pass 1: 256x256, or 128x128 (one workgroup per CU or
+            # fewer: four stages for 16-bit inputs, two for fp32)
+            kern = vk.KERNEL_PIPE256 if tile == 2 else (vk.KERNEL_PIPE128 if dtype == "f32" else vk.KERNEL_PIPE128_4)
+            assert vk.last_kernel() == kern, vk.last_kernel()
             outs.append(to_host(dC))
     finally:
         vk.set_override(-1, False)

@@ -138,8 +138,8 @@ PIPE = {"pipe256": (2, 3, 512, 256), "pipe128x4": (1, 5, 256, 256), "pipe128x2":
 @pytest.mark.parametrize("beta,sep", [(0.0, False), (0.5, True)])
 def test_pipelined(ab, ct, pipe, op_a, op_b, beta, sep):
     tile, kern, M, K = PIPE[pipe]
-    if ab == "f32" and pipe != "pipe256":
-        pytest.skip("the 128x128 pipelined kernel is 16-bit only")
+    if ab == "f32" and kern == 5:
+        kern = 4                                 # fp32 128x128 tiles always run two stages
     run_case(ab, ct, op_a, op_b, M, M, K, 1.25, beta, "f16" if ct == "f16" else "f32", sep, tile=tile,
              expect_kernel=kern)
 

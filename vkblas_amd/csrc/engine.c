@@ -294,7 +294,7 @@ static const char* type_name(int t) {
 }
 
 /* Split-K pass 1 can run on the pipelined kernel: whole tiles of the given
- * tile (256x256, or 128x128 for 16-bit types), K a multiple of two K steps,
+ * tile (256x256 or 128x128), K a multiple of two K steps,
  * 16-byte aligned operands with vector-multiple leading dimensions (the
  * launcher checks the rest and otherwise runs the generic kernel on the same
  * plan). */
@@ -304,7 +304,7 @@ static int pipe_ok(vkblas_dtype_t ab_type, int tile, uint32_t M, uint32_t N, uin
     const uint32_t vec = ab_type == VKBLAS_DT_F32 ? 4 : 8;
     const uint32_t kpair = 2 * vkb_tile_bk(kernel_type(ab_type));
     const uint32_t edge = vkb_tile_bm(tile);
-    if (tile != VKB_TILE_256 && !(tile == VKB_TILE_128 && ab_type != VKBLAS_DT_F32)) return 0;
+    if (tile != VKB_TILE_256 && tile != VKB_TILE_128) return 0;
     return aligned && !g_generic_only && M % edge == 0 && N % edge == 0 && K % kpair == 0 && lda % vec == 0 &&
            ldb % vec == 0;
 }
@@ -364,16 +364,29 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (batch == 1) {
         if (split_k > 1) {
             split = split_k;
-        } else if (split_k == 0 && g_force_tile < 0 && ab_type != VKBLAS_DT_F32 &&
-                   pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
+            /* a caller's split with whole 128x128 tiles that give at least
+             * 224 workgroups: pass 1 on the pipelined 128x128 kernel (at
+             * M = N = 256 with 64 slices, as the planner's own choice below) */
+            if (g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
+                (uint64_t)(M / 128) * (N / 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
+                tile = VKB_TILE_128;
+        } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
                    (uint64_t)(M / 128) * (N / 128) < 64 && K >= 4096) {
-            /* 16-bit inputs (HBM-bound at these shapes): 128x128 tiles, a
-             * workgroup per CU, which the launcher runs with four LDS stages
-             * (three K steps of loads in flight); the tiles of one slice sit
-             * on one XCD and share its A and B reads in L2.  Measured at
+            /* Whole 128x128 tiles, fewer than 64 of them, and a long K: the
+             * pipelined kernel runs pass 1 on 128x128 tiles with 256 / tiles
+             * slices, a workgroup per CU.  Each workgroup reads its A and B
+             * slices once; the tiles of one slice sit on one XCD and share
+             * those reads in L2.
+             * 16-bit inputs (HBM-bound here): the launcher runs four LDS
+             * stages (three K steps of loads in flight).  Measured at
              * M = N = 256, fp16, K = 262144: 54.5 us (4.9 TB/s) against
              * 79.7 us with 256x256 tiles and 128 slices; 32 / 48 / 96 / 128
-             * slices of 128x128: 79.6 / 65.1 / 72.9 / 63.4 us. */
+             * slices of 128x128: 79.6 / 65.1 / 72.9 / 63.4 us.
+             * fp32 (MFMA-bound): at M = N = 256, K = 65536 / 262144, 64
+             * slices take 70.7 / 260.9 us; 32 / 128 / 256 slices 126.9 /
+             * 74.0 / 85.9 and 482.4 / 260.9 / 271.6 us; 256x256 tiles with
+             * 256 slices (a quarter of the K steps per workgroup, four times
+             * the partials) 88.7 / 263.2 us. */
             const uint32_t kpair = 2 * bk;
             const uint64_t t128 = (uint64_t)(M / 128) * (N / 128);
             uint64_t want = 256 / t128;
@@ -383,27 +396,6 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 uint32_t kps = cdiv(cdiv(K, want), kpair) * kpair;
                 split = cdiv(K, kps);
                 tile = VKB_TILE_128;
-            }
-        } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_256, M, N, K, lda, ldb, aligned) &&
-                   (uint64_t)(M / 256) * (N / 256) < 16 && K >= 4096) {
-            /* Few whole 256x256 tiles (where 128x128 tiles would be fewer
-             * than 64 too) and a long K: the pipelined kernel runs pass 1.
-             * Each workgroup reads its A and B slices exactly once, so the
-             * traffic is the operands plus split * M * N * 4 bytes of
-             * partials.  fp32 (MFMA-bound) takes a workgroup per CU
-             * (measured at M = N = 256, K = 65536 / 262144: 256 slices
-             * 91 / 289 us against 136 / 480 at 128); 16-bit inputs get here
-             * only when their dimensions are not multiples of 128, and take
-             * half as many, which halves the partials. */
-            const uint32_t kpair = 2 * bk;
-            const uint64_t t256 = (uint64_t)(M / 256) * (N / 256);
-            uint64_t want = (ab_type == VKBLAS_DT_F32 ? 256 : 128) / t256;
-            uint64_t kmax = K / (PIPE_MIN_STEPS * bk);   /* minimum K steps per slice */
-            if (want > kmax) want = kmax;
-            if (want >= 2) {
-                uint32_t kps = cdiv(cdiv(K, want), kpair) * kpair;
-                split = cdiv(K, kps);
-                tile = VKB_TILE_256;
             }
         } else if (split_k == 0) {
             /* Few output tiles and a long K: split K.  128x128 tiles (reuse

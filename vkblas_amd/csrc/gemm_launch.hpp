@@ -116,11 +116,10 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     const uint32_t grid = (uint32_t)grid64;
     const bool ak = a->a_kmajor != 0, bk = a->b_kmajor != 0;
     {
-        // software-pipelined kernel for full 256x256 tiles, and 128x128 ones
-        // for 16-bit types (also split-K pass 1 on them).  K and the split-K
-        // slice a multiple of two K steps (128 bytes each): the loop runs
-        // pairs.  Buffer offsets are signed 32-bit: bound the byte span of
-        // each operand tile.
+        // software-pipelined kernel for full 256x256 and 128x128 tiles (also
+        // split-K pass 1 on them).  K and the split-K slice a multiple of two
+        // K steps (128 bytes each): the loop runs pairs.  Buffer offsets are
+        // signed 32-bit: bound the byte span of each operand tile.
         constexpr uint64_t ES = sizeof(T);
         constexpr uint32_t KPAIR = 256 / sizeof(T);
         const uint64_t span_a = ((uint64_t)(a->a_kmajor ? bm : a->K) * (uint64_t)a->lda + a->K) * ES;
@@ -138,13 +137,16 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             }
             return (int)hipGetLastError();
         }
-        if constexpr (sizeof(T) == 2) {
-            // 16-bit 128x128 tiles: the pipelined kernel with 64x64 wave tiles;
-            // four LDS stages when the grid is at most one workgroup per CU
-            // (the 144 KB they take allow no second one), else two
-            if (tile == VKB_TILE_128 && pipe_ok) {
-                report(grid <= cu_count() ? VKB_KERN_PIPE128_4 : VKB_KERN_PIPE128);
-                if (grid <= cu_count()) {
+        // 128x128 tiles: the pipelined kernel with 64x64 wave tiles.  16-bit
+        // types take four LDS stages when the grid is at most one workgroup
+        // per CU (the 144 KB they take allow no second one), else two; fp32
+        // (a K step is 4096 MFMA cycles, longer than the load latency) always
+        // two.
+        if (tile == VKB_TILE_128 && pipe_ok) {
+            const bool four = sizeof(T) == 2 && grid <= cu_count();
+            report(four ? VKB_KERN_PIPE128_4 : VKB_KERN_PIPE128);
+            if constexpr (sizeof(T) == 2) {
+                if (four) {
                     if (ak) {
                         if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64, 4>), dim3(grid), dim3(256), 0, st, p);
                         else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64, 4>), dim3(grid), dim3(256), 0, st, p);
@@ -152,15 +154,17 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
                         if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, true, 64, 4>), dim3(grid), dim3(256), 0, st, p);
                         else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false, 64, 4>), dim3(grid), dim3(256), 0, st, p);
                     }
-                } else if (ak) {
-                    if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64>), dim3(grid), dim3(256), 0, st, p);
-                    else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64>), dim3(grid), dim3(256), 0, st, p);
-                } else {
-                    if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, true, 64>), dim3(grid), dim3(256), 0, st, p);
-                    else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false, 64>), dim3(grid), dim3(256), 0, st, p);
+                    return (int)hipGetLastError();
                 }
-                return (int)hipGetLastError();
             }
+            if (ak) {
+                if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, true, 64>), dim3(grid), dim3(256), 0, st, p);
+                else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, true, false, 64>), dim3(grid), dim3(256), 0, st, p);
+            } else {
+                if (bk) hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, true, 64>), dim3(grid), dim3(256), 0, st, p);
+                else hipLaunchKernelGGL((gemm_pipe_kernel<T, TC, false, false, 64>), dim3(grid), dim3(256), 0, st, p);
+            }
+            return (int)hipGetLastError();
         }
     }
     report(full ? VKB_KERN_GENERIC : VKB_KERN_GENERIC_CHECKED);

@@ -1,5 +1,5 @@
 // gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp32, fp16 and
-// bf16, and its 128x128 form for 16-bit types.
+// bf16, and its 128x128 form.
 //
 // Used for full tiles (M, N multiples of the tile, K a multiple of two K
 // steps, aligned operands), also as split-K pass 1 (one K slice per workgroup
@@ -13,10 +13,10 @@
 // 256 AGPRs; WT = 64: 64 AGPRs, two workgroups per CU).  A K step is 128
 // bytes of K (64 fp16 / bf16 or 32 fp32):
 //  * 16-bit types, every layout: two sub-steps of v_mfma_f32_16x16x32 on 8x8
-//    16x16 tiles (64 MFMAs each; lane group g = lane / 16 takes k 8g..8g+7 of
+//    (WT 64: 4x4) 16x16 tiles (lane group g = lane / 16 takes k 8g..8g+7 of
 //    the sub-step's 32);
-//  * fp32: four sub-steps of v_mfma_f32_32x32x2_f32 on 4x4 32x32 tiles (one
-//    MFMA per k of chunk 4h + s, 64 MFMAs each).
+//  * fp32: four sub-steps of v_mfma_f32_32x32x2_f32 on 4x4 (WT 64: 2x2)
+//    32x32 tiles, one MFMA per k of chunk 4h + s.
 // Per K step:
 //  * Operand tiles go global -> LDS directly (buffer_load ... lds: lane l of
 //    a wave writes 16 B at M0 + 16 l), so they use no VGPRs and no ds_write;
@@ -103,8 +103,8 @@ constexpr RdSeq make_rdseq() {
 }
 
 // WT: wave tile edge.  128: 256x256 workgroup tile, one workgroup per CU;
-// 64 (16-bit types): 128x128 workgroup tile for shapes with too few 256x256
-// tiles to fill the chip.
+// 64: 128x128 workgroup tile for shapes with too few 256x256 tiles to fill
+// the chip (fp32 always with two stages).
 // NST: LDS stages.  2: the DMA of a K step is issued one step ahead.  4
 // (WT 64 only, 144 KB: one workgroup per CU, for grids of at most one
 // workgroup per CU): three steps ahead, since a 128x128 step (512 MFMA
@@ -112,8 +112,8 @@ constexpr RdSeq make_rdseq() {
 template <typename T, typename TC, bool AK, bool BKM, int WT = 128, int NST = 2>
 __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pipe_kernel(KParams p) {
     constexpr bool F16 = sizeof(T) == 2;
-    static_assert(WT == 128 || (WT == 64 && F16), "128x128 tiles are 16-bit only");
-    static_assert(NST == 2 || (NST == 4 && WT == 64), "four stages only fit 128x128 tiles");
+    static_assert(WT == 128 || WT == 64, "256x256 or 128x128 tiles");
+    static_assert(NST == 2 || (NST == 4 && WT == 64 && F16), "four stages: 16-bit 128x128 tiles only");
     constexpr int ES = sizeof(T);                   // element bytes
     constexpr int BM = 2 * WT, BN = 2 * WT, BK = 128 / ES;
     constexpr int VEC = 16 / ES;                    // elements per 16-byte chunk
@@ -205,13 +205,14 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // outstanding load; the "memory" clobber keeps the compiler from moving
     // LDS accesses across it.
     constexpr bool STAGED = !F16 && (!AK || !BKM);  // fp32 MN-major operand through VGPRs
-    constexpr int NSTAGED = STAGED ? (AK ? 0 : 8) + (BKM ? 0 : 8) : 0;
+    constexpr int NSV = BM / 32;                    // staged loads per MN-major operand and K step
+    constexpr int NSTAGED = STAGED ? (AK ? 0 : NSV) + (BKM ? 0 : NSV) : 0;
     auto sync_vm = [](auto n_c) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(decltype(n_c)::value) : "memory");
     };
 
     // staged registers: index blk * VEC + k row within the block
-    u32x4 sa_v[(STAGED && !AK) ? 8 : 1], sb_v[(STAGED && !BKM) ? 8 : 1];
+    u32x4 sa_v[(STAGED && !AK) ? NSV : 1], sb_v[(STAGED && !BKM) ? NSV : 1];
 
     // With a transposed-read operand or more than two stages every DMA is
     // issued as inline assembly.  The compiler waits for all LDS DMA in
@@ -258,7 +259,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
                     (k0 + RPB * (NDMA * wave + m)) * ldb * ES);
         }
     };
-    // MN-major staged load v of K step kt (8 per operand)
+    // MN-major staged load v of K step kt (NSV per operand)
     auto stage_load = [&](int kt, int v) {
         const int k0 = kt * BK + (v % VEC);
         const int blk = v / VEC;
@@ -282,11 +283,11 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     //   data gfx950 sustains ~15% more fp16 FLOP/s on 16x16x32 than on
     //   32x32x16 (half the accumulator traffic per FLOP under the power limit).
     // SH 2, fp32: v_mfma_f32_32x32x2_f32, sub-step s = chunk 4h + s (one MFMA
-    //   per k), 4x4 tiles of 32x32.
+    //   per k), NF x NF tiles of 32x32 (4x4 for WT 128, 2x2 for WT 64).
     constexpr int SH = F16 ? 0 : 2;
     constexpr int NSUB = SH == 0 ? 2 : 4;           // sub-steps per K step
     constexpr int UPS = 32 / NSUB;                  // units per sub-step
-    constexpr int NF = SH == 0 ? WT / 16 : 4;       // fragments per operand
+    constexpr int NF = WT / (SH == 0 ? 16 : 32);    // fragments per operand
     constexpr int MPU = NF * NF / 16;               // MFMAs per unit (SH 0)
     constexpr int FR = SH == 0 ? 16 : 32;           // rows per fragment
     constexpr int SX = SH == 0 ? 4 : 1;             // sub-step slot offset
@@ -360,9 +361,10 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     //   unit 2i+1 and its successor is read in that unit or a later one, so A
     //   needs one register set; otherwise A is read earlier and takes two, as
     //   B always does.
-    // SH 2: unit q = k element q/2 of the chunk on tiles (2(q%2) .. +1, 0..3):
-    //   reads B0..B3 A0..A3, every fragment kept to the sub-step's end: two
-    //   sets each.
+    // SH 2: unit q = k element q/2 of the chunk on tile rows (NF/2)(q%2) ..
+    //   +NF/2 - 1, all NF columns: units 0 .. 2 NF - 1 read B0 .. B(NF-1), then
+    //   A0 .. A(NF-1), every fragment kept to the sub-step's end: two sets
+    //   each.
     constexpr int NAB = (SH == 0 && !ATR && WT == 128) ? 1 : 2;
     constexpr int NRD = 2 * NF + (ATR ? NF : 0) + (BTR ? NF : 0);   // SH 0 reads per sub-step
     u32x4 af[NAB][NF], bf[2][NF];
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
                 }
             }
         } else {
-            frag_read(buf, S, s, q >= 4, q & 3, 0);
+            if (q < 2 * NF) frag_read(buf, S, s, q >= NF, q % NF, 0);
         }
     };
     auto mfma_unit = [&](int buf, int q) {
@@ -406,11 +408,11 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             for (int j = j0; j < j0 + MPU; ++j)
                 acc[i][j] = mfma_16x16x32<T>(bf[buf][j], af[buf % NAB][i], acc[i][j]);
         } else {
-            const int e = q >> 1, i0 = (q & 1) * 2;
+            const int e = q >> 1, i0 = (q & 1) * (NF / 2);
 #pragma unroll
-            for (int i = i0; i < i0 + 2; ++i)
+            for (int i = i0; i < i0 + NF / 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+                for (int j = 0; j < NF; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(bf[buf][j][e]),
                                                                     __uint_as_float(af[buf % NAB][i][e]), acc[i][j],
                                                                     0, 0, 0);
@@ -422,8 +424,8 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // kt.  The ND DMA loads of kt+1 are spread over DMA_UNITS units from the
     // first (issued in a burst they oversubscribe the texture address unit
     // and stall the MFMA issue); staged MN-major rows of kt+1 are written in
-    // units [16, 24) and the staged loads of kt+2 issued in [24, 32), after
-    // every DMA, which the end-of-region wait relies on.  The first region
+    // units [16, 16 + NSV) and the staged loads of kt+2 issued in [24, 24 +
+    // NSV), after every DMA, which the end-of-region wait relies on.  The first region
     // has no previous sub-step: its units start at UPS and its DMA is spread
     // over [UPS, 24).
     // 16-bit 256x256 tiles with K-major A and transposed-read B: 24 units
@@ -459,8 +461,8 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             mfma_unit(buf, q);
             read_one((sub + 1) & 1, S, sub + 1, q);
             if (next) dma_unit(kt + NST - 1, (S + NST - 1) % NST, u, prev);
-            if (STAGED && next && u >= 16 && u < 24) stage_store(S ^ 1, u - 16);
-            if (STAGED && next2 && u >= 24) stage_load(kt + 2, u - 24);
+            if (STAGED && next && u >= 16 && u < 16 + NSV) stage_store(S ^ 1, u - 16);
+            if (STAGED && next2 && u >= 24 && u < 24 + NSV) stage_load(kt + 2, u - 24);
             __builtin_amdgcn_sched_barrier(0);
         }
         sync_vm(wc);
@@ -472,7 +474,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     if constexpr (STAGED) {
         // MN-major first, so waiting for them leaves the direct loads in flight
 #pragma unroll
-        for (int v = 0; v < 8; ++v) stage_load(0, v);
+        for (int v = 0; v < NSV; ++v) stage_load(0, v);
     }
 #pragma unroll
     for (int n = 0; n < ND; ++n) dma_load(0, 0, n);
@@ -490,9 +492,9 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     } else {
         if constexpr (STAGED) {
 #pragma unroll
-            for (int v = 0; v < 8; ++v) stage_store(0, v);
+            for (int v = 0; v < NSV; ++v) stage_store(0, v);
 #pragma unroll
-            for (int v = 0; v < 8; ++v) stage_load(1, v);   // nkt >= 2
+            for (int v = 0; v < NSV; ++v) stage_load(1, v);   // nkt >= 2
         }
         sync_vm(WS{});
     }
