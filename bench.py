@@ -13,7 +13,7 @@ copies rotated so the 256 MB Infinity Cache cannot serve them), a roofline
 object for the dominant kernel and the CPU comparator.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--only fp32|fp16|bf16|matvec|matvec_ns|bf16mv|f32mv|splitk|batched|ceiling|vendor]
+                  [--only fp32|fp16|bf16|matvec|matvec_ns|bf16mv|f32mv|splitk|batched|shapes|ceiling|vendor]
 """
 import argparse
 import json
@@ -179,6 +179,34 @@ def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
     return out
 
 
+def shapes(torch, vk, stream, steps):
+    """Square GEMMs off the BASELINE sizes, NN and TN through the planner:
+    fp32 where 128x128 tiles fill the chip (2048^3, 3072^3) or leave no
+    partial wave (5120^3, 6144^3), fp16 3072^3 (144 tiles of 256x256)."""
+    out = {}
+    sp = stream.cuda_stream
+    for dtn, n in (("f32", 2048), ("f32", 3072), ("f32", 5120), ("f32", 6144), ("f16", 3072)):
+        g = torch.Generator(device="cuda:0").manual_seed(11)
+        A = torch.rand(n * n, device="cuda:0", generator=g) * 2 - 1
+        B = torch.rand(n * n, device="cuda:0", generator=g) * 2 - 1
+        if dtn == "f16":
+            A, B = A.half(), B.half()
+        C = torch.empty(n * n, device="cuda:0", dtype=A.dtype)
+        vdt = vk.DT_F16 if dtn == "f16" else vk.DT_F32
+        peak = PEAK_FP16_TFLOPS if dtn == "f16" else PEAK_FP32_TFLOPS
+        for name, ta in (("NN", 0), ("TN", 1)):
+            def call():
+                vk.gemm_async(vdt, vdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
+                              C.data_ptr(), n, stream=sp)
+            warm(torch, lambda i: call())
+            med = batch_ms(torch, stream, lambda i: call(), max(steps, 10))
+            tf = 2.0 * n ** 3 / (med * 1e-3) / 1e12
+            out[f"{dtn}_{n}_{name}"] = {"ms": round(med, 4), "tflops": round(tf, 1),
+                                         "path": vk.PATH_NAMES[vk.last_path()], "frac_of_peak": round(tf / peak, 4)}
+        del A, B, C
+    return out
+
+
 def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=False):
     """configs[3]: decode GemmEx(T, N, m=O, n=ntok, k=K), W K-contiguous;
     three weight copies (3 x 128 MiB > 256 MB MALL) rotated per launch
@@ -298,7 +326,7 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "matvec_ns", "bf16mv", "f32mv", "splitk", "batched",
-                                       "calibrate", "ceiling", "vendor"],
+                                       "shapes", "calibrate", "ceiling", "vendor"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -339,6 +367,9 @@ def main():
         return
     if args.only == "batched":
         print(json.dumps(batched(torch, vk, stream, args.steps)))
+        return
+    if args.only == "shapes":
+        print(json.dumps(shapes(torch, vk, stream, args.steps)))
         return
     if args.only == "vendor":
         print(json.dumps(vendor(torch, vk, stream, args.steps)))
@@ -406,6 +437,8 @@ def main():
     log("[bench] split-K and strided-batched")
     line["splitk_256x256"] = splitk(torch, vk, stream, args.steps)
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
+    log("[bench] square GEMMs off the BASELINE sizes")
+    line["more_shapes"] = shapes(torch, vk, stream, args.steps)
     if not args.no_cpu:
         # last, so the GPU legs run back to back without an idle gap between them
         log("[bench] cpu baseline")

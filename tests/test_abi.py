@@ -176,6 +176,26 @@ def test_plan_headline_configs():
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 512, 512, 512, 512, 512, 512, batch=64).split == 1
 
 
+def test_plan_tile_crossover():
+    """Square shapes where both pipelined tile sizes apply: fp32 keeps
+    256x256 tiles only for about whole waves of one workgroup per CU; 16-bit
+    inputs take them from 128 tiles on."""
+    def tile(dt, n, batch=1):
+        pl = P(dt, dt, 0, 0, n, n, n, n, n, n, batch=batch)
+        assert pl.split == 1
+        return pl.path
+    T128, T256 = vk.PATH_TILE128, vk.PATH_TILE256
+    assert [tile(vk.DT_F32, n) for n in (2048, 3072, 4096, 5120, 6144, 8192)] == [T128, T128, T256, T128, T128, T256]
+    assert tile(vk.DT_F32, 512, batch=64) == T256          # 256 tiles: one whole wave
+    assert tile(vk.DT_F32, 512, batch=60) == T256          # 240 of 256
+    assert tile(vk.DT_F32, 512, batch=50) == T128          # 200 of 256
+    for dt in (vk.DT_F16, vk.DT_BF16):
+        assert [tile(dt, n) for n in (2048, 2560, 2816, 3072, 3584, 4096, 6144)] == [T128, T128, T128, T256, T256,
+                                                                                      T256, T256]
+    # a shape only the generic kernels take keeps the size rule (fp32 5000^3: 256x256 tiles)
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 5000, 5000, 5000, 5000, 5000, 5000).path == T256
+
+
 def test_plan_decode_split():
     """Decode K split: up to 16 tokens none; from 17 tokens the largest split
     that keeps the grid (128 weight rows per workgroup) within one round of

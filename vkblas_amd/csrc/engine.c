@@ -360,6 +360,26 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
 
     const uint32_t bk = vkb_tile_bk(kernel_type(ab_type));
     int tile = choose_tile(M, N, batch);
+    if (g_force_tile < 0) {
+        /* Where both pipelined tile sizes apply, the measured crossovers
+         * (square shapes, NN and NT, one box):
+         * - fp32: 128x128 tiles are never slower, and faster wherever
+         *   256x256 tiles leave a partial wave of one workgroup per CU
+         *   (5120^3 131.5 against 116.3 TFLOP/s, 6144^3 147.7 / 110.9;
+         *   4096^3 and the 64 x 512^3 batch equal): 256x256 only for about
+         *   whole waves.
+         * - 16-bit: 256x256 tiles from 128 of them on (3072^3 fp16 963 against
+         *   793 TFLOP/s, 3584^3 1154-1245 / 1017-1048; 2560^3, 100 tiles:
+         *   656 against 989). */
+        const uint64_t t256 = (uint64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
+        if (ab_type == VKBLAS_DT_F32 && tile == VKB_TILE_256 &&
+            pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
+            8 * t256 < 7 * 256 * ((t256 + 255) / 256))
+            tile = VKB_TILE_128;
+        if (ab_type != VKBLAS_DT_F32 && tile == VKB_TILE_128 && t256 >= 128 &&
+            pipe_ok(ab_type, VKB_TILE_256, M, N, K, lda, ldb, aligned))
+            tile = VKB_TILE_256;
+    }
     uint32_t split = 1;
     if (batch == 1) {
         if (split_k > 1) {
