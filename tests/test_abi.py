@@ -295,9 +295,13 @@ def test_plan_split_heuristic_and_off():
     # 16-bit inputs: the same
     pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 262144, 262144, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 128 == 0 and 4 * pl.split <= 256
-    # ragged M: the 128x128 generic split
+    # ragged M: 128x128 tiles (the pipelined pass 1 with a shifted edge tile),
+    # slices of whole K-step pairs
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 256, 65536, 65536, 256, 256)
-    assert pl.path == vk.PATH_SPLITK and pl.tile == 1
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 64 == 0 and 4 * pl.split <= 256
+    # below the tile in M: the generic 64x64 split
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 100, 256, 65536, 65536, 256, 256)
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 0
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=1)
     assert pl.path != vk.PATH_SPLITK
     # batched calls never split

@@ -293,20 +293,23 @@ static const char* type_name(int t) {
     return t == VKB_T_F16 ? "f16" : t == VKB_T_BF16 ? "bf16" : "f32";
 }
 
-/* Split-K pass 1 can run on the pipelined kernel: whole tiles of the given
- * tile (256x256 or 128x128), K a multiple of two K steps,
- * 16-byte aligned operands with vector-multiple leading dimensions (the
- * launcher checks the rest and otherwise runs the generic kernel on the same
- * plan). */
+/* The pipelined kernel runs the given tile (256x256 or 128x128): M and N at
+ * least the tile (edge tiles shift back inside the matrix), N % 4 == 0, the
+ * ragged dimension of an MN-major operand (A with op_a = T, B with op_b = N)
+ * a multiple of 16 bytes, K a multiple of two K steps, 16-byte aligned
+ * operands with vector-multiple leading dimensions.  The launcher checks the
+ * rest (C alignment, 32-bit spans) and otherwise runs the generic kernel on
+ * the same plan. */
 #define PIPE_MIN_STEPS 4u
-static int pipe_ok(vkblas_dtype_t ab_type, int tile, uint32_t M, uint32_t N, uint32_t K, uint32_t lda,
-                   uint32_t ldb, int aligned) {
+static int pipe_ok(vkblas_dtype_t ab_type, int tile, vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N,
+                   uint32_t K, uint32_t lda, uint32_t ldb, int aligned) {
     const uint32_t vec = ab_type == VKBLAS_DT_F32 ? 4 : 8;
     const uint32_t kpair = 2 * vkb_tile_bk(kernel_type(ab_type));
     const uint32_t edge = vkb_tile_bm(tile);
     if (tile != VKB_TILE_256 && tile != VKB_TILE_128) return 0;
-    return aligned && !g_generic_only && M % edge == 0 && N % edge == 0 && K % kpair == 0 && lda % vec == 0 &&
-           ldb % vec == 0;
+    return aligned && !g_generic_only && M >= edge && N >= edge && N % 4 == 0 &&
+           (op_a == VKBLAS_OP_N || M % vec == 0) && (op_b == VKBLAS_OP_T || N % vec == 0) && K % kpair == 0 &&
+           lda % vec == 0 && ldb % vec == 0;
 }
 
 /* Tile choice for 256 CUs: the largest tile that still gives about one
@@ -373,11 +376,11 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
          *   656 against 989). */
         const uint64_t t256 = (uint64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
         if (ab_type == VKBLAS_DT_F32 && tile == VKB_TILE_256 &&
-            pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
+            pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
             8 * t256 < 7 * 256 * ((t256 + 255) / 256))
             tile = VKB_TILE_128;
         if (ab_type != VKBLAS_DT_F32 && tile == VKB_TILE_128 && t256 >= 128 &&
-            pipe_ok(ab_type, VKB_TILE_256, M, N, K, lda, ldb, aligned))
+            pipe_ok(ab_type, VKB_TILE_256, op_a, op_b, M, N, K, lda, ldb, aligned))
             tile = VKB_TILE_256;
     }
     uint32_t split = 1;
@@ -387,11 +390,11 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             /* a caller's split with whole 128x128 tiles that give at least
              * 224 workgroups: pass 1 on the pipelined 128x128 kernel (at
              * M = N = 256 with 64 slices, as the planner's own choice below) */
-            if (g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
-                (uint64_t)(M / 128) * (N / 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
+            if (g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
+                (uint64_t)cdiv(M, 128) * cdiv(N, 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
                 tile = VKB_TILE_128;
-        } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, M, N, K, lda, ldb, aligned) &&
-                   (uint64_t)(M / 128) * (N / 128) < 64 && K >= 4096) {
+        } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
+                   (uint64_t)cdiv(M, 128) * cdiv(N, 128) < 64 && K >= 4096) {
             /* Whole 128x128 tiles, fewer than 64 of them, and a long K: the
              * pipelined kernel runs pass 1 on 128x128 tiles with 256 / tiles
              * slices, a workgroup per CU.  Each workgroup reads its A and B
@@ -408,7 +411,7 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
              * 256 slices (a quarter of the K steps per workgroup, four times
              * the partials) 88.7 / 263.2 us. */
             const uint32_t kpair = 2 * bk;
-            const uint64_t t128 = (uint64_t)(M / 128) * (N / 128);
+            const uint64_t t128 = (uint64_t)cdiv(M, 128) * cdiv(N, 128);
             uint64_t want = 256 / t128;
             uint64_t kmax = K / (PIPE_MIN_STEPS * bk);
             if (want > kmax) want = kmax;
@@ -440,7 +443,7 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     }
     if (split > 1) {
         /* slices of whole K steps; of whole step pairs for the pipelined kernel */
-        const int pipe = pipe_ok(ab_type, tile, M, N, K, lda, ldb, aligned);
+        const int pipe = pipe_ok(ab_type, tile, op_a, op_b, M, N, K, lda, ldb, aligned);
         const uint32_t gran = pipe ? 2 * bk : bk;
         uint32_t kps = cdiv(cdiv(K, split), gran) * gran;
         split = cdiv(K, kps);                     /* every slice non-empty */

@@ -101,8 +101,10 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     }
     {
         constexpr int64_t CV = 16 / sizeof(TC);   // elements per 16 bytes of C
+        // an edge tile (N not a multiple of the tile) stores from a shifted
+        // column N - BN on: whole 16-byte chunks need N % CV == 0 as well
         p.c_rows16 = !p.ptr_array && a->ldc % CV == 0 && aligned(a->C, 16) && (!multi || a->stride_c % CV == 0) &&
-                     (p.split == 1 || p.s_split % CV == 0);
+                     (p.split == 1 || p.s_split % CV == 0) && (a->N % bn == 0 || a->N % CV == 0);
     }
     auto report = [&](int k) {
         if (a->kernel_out) *a->kernel_out = k;
@@ -120,11 +122,19 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
         // split-K pass 1 on them).  K and the split-K slice a multiple of two
         // K steps (128 bytes each): the loop runs pairs.  Buffer offsets are
         // signed 32-bit: bound the byte span of each operand tile.
+        // Edge tiles (M or N not a multiple of the tile) shift back inside
+        // the matrix: M >= bm, N >= bn; the shifted start of an MN-major
+        // operand stays 16-byte aligned (M or N a multiple of VEC); the
+        // epilogue masks groups of four columns (N % 4 == 0).
         constexpr uint64_t ES = sizeof(T);
         constexpr uint32_t KPAIR = 256 / sizeof(T);
         const uint64_t span_a = ((uint64_t)(a->a_kmajor ? bm : a->K) * (uint64_t)a->lda + a->K) * ES;
         const uint64_t span_b = ((uint64_t)(a->b_kmajor ? bn : a->K) * (uint64_t)a->ldb + a->K) * ES;
-        const bool pipe_ok = full && (p.split == 1 || p.kps % KPAIR == 0) && !a->generic_only &&
+        const bool edges_ok = a->M >= (uint32_t)bm && a->N >= (uint32_t)bn && a->N % 4 == 0 &&
+                              (a->a_kmajor || a->M % VEC == 0) && (a->b_kmajor || a->N % VEC == 0);
+        const bool tiles_ok = !p.ptr_array && (a->K % BK == 0) && p.vec_a && p.vec_b && p.vec_c &&
+                              (full || edges_ok);
+        const bool pipe_ok = tiles_ok && (p.split == 1 || p.kps % KPAIR == 0) && !a->generic_only &&
                              a->K % KPAIR == 0 && span_a < (1ull << 31) && span_b < (1ull << 31);
         if (tile == VKB_TILE_256 && pipe_ok) {
             report(VKB_KERN_PIPE256);

@@ -1,9 +1,10 @@
 // gemm_pipe.hpp — software-pipelined 256x256 GEMM for gfx950, fp32, fp16 and
 // bf16, and its 128x128 form.
 //
-// Used for full tiles (M, N multiples of the tile, K a multiple of two K
-// steps, aligned operands), also as split-K pass 1 (one K slice per workgroup
-// row of the grid, raw fp32 sums); edges and small shapes use gemm_kernel<> in
+// Used where M, N >= the tile (edge tiles move back inside the matrix and
+// mask their stores), K is a multiple of two K steps and the operands are
+// aligned; also as split-K pass 1 (one K slice per workgroup row of the grid,
+// raw fp32 sums).  Small and unaligned shapes use gemm_kernel<> in
 // gemm_mfma.hpp, whose MFMA role swap and epilogue this kernel shares.
 // Replaces the reference's large tiles (gemm_f32_128x128_bankfree_tmpl.comp,
 // gemm_half_128x256_bankfree_tmpl.comp, gemm_half_128x128_bankfree_tmpl.comp,
@@ -146,8 +147,16 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     const uint32_t first_m = group * GM;
     const uint32_t gm = min(p.tiles_m - first_m, GM);
     const uint32_t tin = t - group * width;
-    const int m0 = (int)(first_m + tin % gm) * BM;
-    const int n0 = (int)(tin / gm) * BN;
+    // Edge tiles (M or N not a multiple of the tile, M >= BM and N >= BN:
+    // the launcher checks) move back inside the matrix, so every load stays
+    // in bounds: the last tile row computes rows M - BM .. M - 1 and stores
+    // only those from its own start m_lo on, which the tile before it does
+    // not store (likewise for columns).  Nothing is stored twice, so beta
+    // != 0 reads each C element once.
+    const int m_lo = (int)(first_m + tin % gm) * BM;
+    const int n_lo = (int)(tin / gm) * BN;
+    const int m0 = min(m_lo, (int)p.M - BM);
+    const int n0 = min(n_lo, (int)p.N - BN);
 
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     // Split-K pass 1 (split > 1, batch 1): slice b covers k in
@@ -623,7 +632,12 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             for (int it = 0; it < PROWS * LPR / 64; ++it) {
                 const int r = it * (64 / LPR) + lane / LPR, c = lane % LPR;
                 const u32x4 v = *(const u32x4*)(wl + r * STR + c * 16);
-                __builtin_nontemporal_store(v, (u32x4*)((char*)(cblk + (int64_t)(pass * PROWS + r) * p.ldc) + c * 16));
+                // an edge tile's chunks start on n_lo: the launcher takes this
+                // path only where N is a multiple of 16 bytes of C
+                const bool mine = m0 + wm * WT + pass * PROWS + r >= m_lo &&
+                                  n0 + wn * WT + c * (16 / (int)sizeof(TC)) >= n_lo;
+                if (mine)
+                    __builtin_nontemporal_store(v, (u32x4*)((char*)(cblk + (int64_t)(pass * PROWS + r) * p.ldc) + c * 16));
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
@@ -638,6 +652,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int m = m0 + wm * WT + i * FR + fl;
+            if (m < m_lo) continue;   // stored by the tile before an edge tile
             TC* crow = Cb + (int64_t)m * p.ldc;
             const TC* cirow = Ci + (int64_t)m * p.epi.ldcin;
 #pragma unroll
@@ -645,6 +660,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
 #pragma unroll
                 for (int q = 0; q < NQ; ++q) {
                     const int n = n0 + wn * WT + j * FR + (SH == 0 ? 4 * (lane >> 4) : q * 8 + h * 4);
+                    if (n < n_lo) continue;   // N % 4 == 0: a group of four is all below n_lo or none
                     float x[4], o[4] = {0.f, 0.f, 0.f, 0.f};
                     if (rd) load4<TC>(cirow + n, o, true);
 #pragma unroll
