@@ -180,29 +180,37 @@ def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
 
 
 def shapes(torch, vk, stream, steps):
-    """Square GEMMs off the BASELINE sizes, NN and TN through the planner:
-    fp32 where 128x128 tiles fill the chip (2048^3, 3072^3) or leave no
-    partial wave (5120^3, 6144^3), fp16 3072^3 (144 tiles of 256x256)."""
+    """GEMMs off the BASELINE sizes, hipBLAS NN and TN (column-major m x n x
+    k) through the planner: fp32 squares where 128x128 tiles fill the chip
+    (2048^3, 3072^3) or leave no partial wave (5120^3, 6144^3), fp16 3072^3
+    (144 tiles of 256x256), and ragged shapes on the pipelined kernel's
+    shifted edge tiles (m = 4000, a 2047-token fp16 projection)."""
     out = {}
     sp = stream.cuda_stream
-    for dtn, n in (("f32", 2048), ("f32", 3072), ("f32", 5120), ("f32", 6144), ("f16", 3072)):
+    cases = [("f32", 2048, 2048, 2048), ("f32", 3072, 3072, 3072), ("f32", 5120, 5120, 5120),
+             ("f32", 6144, 6144, 6144), ("f16", 3072, 3072, 3072), ("f32", 4000, 4000, 4096),
+             ("f16", 4000, 4000, 4096), ("f16", 14336, 2047, 4096)]
+    for dtn, m, n, k in cases:
         g = torch.Generator(device="cuda:0").manual_seed(11)
-        A = torch.rand(n * n, device="cuda:0", generator=g) * 2 - 1
-        B = torch.rand(n * n, device="cuda:0", generator=g) * 2 - 1
+        A = torch.rand(m * k, device="cuda:0", generator=g) * 2 - 1
+        B = torch.rand(k * n, device="cuda:0", generator=g) * 2 - 1
         if dtn == "f16":
             A, B = A.half(), B.half()
-        C = torch.empty(n * n, device="cuda:0", dtype=A.dtype)
+        C = torch.empty(m * n, device="cuda:0", dtype=A.dtype)
         vdt = vk.DT_F16 if dtn == "f16" else vk.DT_F32
         peak = PEAK_FP16_TFLOPS if dtn == "f16" else PEAK_FP32_TFLOPS
         for name, ta in (("NN", 0), ("TN", 1)):
+            # column-major C (m x n) = op(A) B: the engine computes the
+            # row-major n x m product with A and B swapped
             def call():
-                vk.gemm_async(vdt, vdt, vk.OP_N, ta, n, n, n, 1.0, B.data_ptr(), n, A.data_ptr(), n, 0.0,
-                              C.data_ptr(), n, stream=sp)
+                vk.gemm_async(vdt, vdt, vk.OP_N, ta, n, m, k, 1.0, B.data_ptr(), k, A.data_ptr(), k if ta else m,
+                              0.0, C.data_ptr(), m, stream=sp)
             warm(torch, lambda i: call())
             med = batch_ms(torch, stream, lambda i: call(), max(steps, 10))
-            tf = 2.0 * n ** 3 / (med * 1e-3) / 1e12
-            out[f"{dtn}_{n}_{name}"] = {"ms": round(med, 4), "tflops": round(tf, 1),
-                                         "path": vk.PATH_NAMES[vk.last_path()], "frac_of_peak": round(tf / peak, 4)}
+            tf = 2.0 * m * n * k / (med * 1e-3) / 1e12
+            key = f"{dtn}_{m}" if m == n == k else f"{dtn}_{m}x{n}x{k}"
+            out[f"{key}_{name}"] = {"ms": round(med, 4), "tflops": round(tf, 1),
+                                    "path": vk.PATH_NAMES[vk.last_path()], "frac_of_peak": round(tf / peak, 4)}
         del A, B, C
     return out
 
