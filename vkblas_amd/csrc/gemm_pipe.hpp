@@ -17,14 +17,17 @@
 //    (WT 64: 4x4) 16x16 tiles (lane group g = lane / 16 takes k 8g..8g+7 of
 //    the sub-step's 32);
 //  * fp32: four sub-steps of v_mfma_f32_32x32x2_f32 on 4x4 (WT 64: 2x2)
-//    32x32 tiles, one MFMA per k of chunk 4h + s.
+//    32x32 tiles; MFMA e of sub-step s takes k = 8 s + e from lanes 0-31 and
+//    k = 8 s + 4 + e from lanes 32-63.
 // Per K step:
 //  * Operand tiles go global -> LDS directly (buffer_load ... lds: lane l of
 //    a wave writes 16 B at M0 + 16 l), so they use no VGPRs and no ds_write;
 //    lane l fetches the global chunk that the LDS swizzle maps to its slot,
-//    so the global side stays fully coalesced.  Exception: an fp32 MN-major
-//    operand goes through VGPRs (VEC x VEC blocks transposed in registers and
-//    written K-contiguous, 8 ds_write_b128 per lane).
+//    so the global side stays fully coalesced.
+//  * An fp32 MN-major operand stays MN-major in LDS: the 32x32x2 MFMA takes
+//    one element per lane and k, and 32 lanes of one k row read 32
+//    consecutive m, so its fragments are ds_read_b32 of whole 128-byte row
+//    segments.
 //  * A 16-bit MN-major operand stays MN-major in LDS and its fragments are
 //    read with ds_read_b64_tr_b16: within each 16-lane group, lane i receives
 //    element i & 3 of the 8 bytes addressed by lanes (i >> 2) + 4 j, j = 0..3.
@@ -41,9 +44,12 @@
 // ds_read_b128 16 lanes at a time, so the 16 rows a fragment read touches at
 // one chunk must land on 16 distinct 16-byte bank groups: the 8 rows of one
 // row parity share a 256-byte bank line half and need 8 distinct slots.
-//  * fp32 MN-major tiles (written transposed through VGPRs): row r at r*8,
-//    chunk c at slot c ^ g(r), g(r) = (r ^ (r >> 3)) & 7 — over 16
-//    consecutive rows each parity class sees all 8 slots.
+//  * fp32 MN-major tiles (k rows of BM m, unswizzled): BM 256: row k at
+//    k * 1056 bytes (one DMA instruction per row); BM 128: rows k, k+1 form
+//    a 1-KiB block (one instruction) at (k >> 1) * 1088, row k & 1 at +512.
+//    A fragment read has lanes 0-31 on row k and lanes 32-63 on row k + 4:
+//    4 * 1056 and 2 * 1088 are 128 modulo 256, so the two 128-byte segments
+//    fall on the two halves of the 64 banks.
 //  * K-major tiles (written by whole-row DMA, lane l -> +16 l, so the swizzle
 //    can only depend on r & 7): chunk c of row r at slot c ^ (r & 7), rows
 //    in groups of 8 at (r >> 3)*GRP + (r & 7)*8.  16-bit types read 16-row
@@ -62,7 +68,7 @@
 //    16-byte bank groups.  t(k + 4) = t(k) for the second read and
 //    t(k + 32) = t(k) for the second sub-step, so both are immediate offsets.
 // Every row base has its low three bits clear, so a fragment's slot index is
-// (base + (hoff ^ g)) ^ sub-step offset (4s, 2s or s by MFMA shape).
+// (base + (hoff ^ g)) ^ sub-step offset (4s for 16-bit types, 2s for fp32).
 //
 // Global traffic uses buffer loads on resources based at the tile's first
 // element: a fixed per-lane VGPR offset plus a uniform SGPR offset (row step
@@ -78,6 +84,7 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
+typedef __attribute__((address_space(3))) const uint32_t lds_u32_t;
 
 #ifndef VKB_PIPE_DMA_UNITS
 #define VKB_PIPE_DMA_UNITS 16
@@ -117,7 +124,6 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     static_assert(NST == 2 || (NST == 4 && WT == 64 && F16), "four stages: 16-bit 128x128 tiles only");
     constexpr int ES = sizeof(T);                   // element bytes
     constexpr int BM = 2 * WT, BN = 2 * WT, BK = 128 / ES;
-    constexpr int VEC = 16 / ES;                    // elements per 16-byte chunk
     constexpr int NDMA = BM / 32;                   // DMA instructions per operand, wave and K step
     constexpr int CPR = BM / 8;                     // 16-byte chunks of an MN-major k row
     constexpr int RPB = 64 / CPR;                   // k rows per 1-KiB transposed-read block
@@ -202,26 +208,26 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
         a_tr[v] = r * lda * ES + (((lane % CPR) ^ tsw(k)) << 4);
         b_tr[v] = r * ldb * ES + (((lane % CPR) ^ tsw(k)) << 4);
     }
-    // MN-major staged loads: VECxVEC blocks (kb, mb + 32 blk), kb = tid / 32
-    // (k rows kb*VEC..), mb = tid % 32 (columns (mb + 32 blk)*VEC..)
-    const int kb = tid >> 5, mb = tid & 31;
-    auto mn_off = [&](int ld, int blk) { return ((kb * VEC) * ld + (mb + 32 * blk) * VEC) * ES; };
+    // fp32 MN-major direct loads: instruction n of this wave fills k row
+    // NDMA wave + n (BM 256: lane -> m chunk lane) or the two-row block
+    // NDMA wave + n (BM 128: lane -> row lane / 32, m chunk lane % 32); one
+    // VGPR offset serves every instruction, the row and k0 go in soffset.
+    constexpr bool AMN = !F16 && !AK, BMN = !F16 && !BKM;
+    constexpr int MNB = BM == 256 ? 66 : 68;        // u32x4 units per row (BM 256) or row pair (BM 128)
+    constexpr int MNR = BM == 256 ? 1 : 2;          // k rows per DMA instruction
+    auto mn_unit = [](int k) { return BM == 256 ? k * 66 : (k >> 1) * 68 + (k & 1) * 32; };
+    const int a_mnoff = BM == 256 ? lane * 16 : (lane >> 5) * lda * ES + (lane & 31) * 16;
+    const int b_mnoff = BM == 256 ? lane * 16 : (lane >> 5) * ldb * ES + (lane & 31) * 16;
 
-    // Barrier after "s_waitcnt vmcnt(n) lgkmcnt(0)": the staged loads issued
-    // after a K step's DMA may stay in flight; vector loads complete in issue
-    // order, so this still waits for the DMA.  The barrier is written out
-    // (no __syncthreads) because its workgroup fence would wait for every
-    // outstanding load; the "memory" clobber keeps the compiler from moving
-    // LDS accesses across it.
-    constexpr bool STAGED = !F16 && (!AK || !BKM);  // fp32 MN-major operand through VGPRs
-    constexpr int NSV = BM / 32;                    // staged loads per MN-major operand and K step
-    constexpr int NSTAGED = STAGED ? (AK ? 0 : NSV) + (BKM ? 0 : NSV) : 0;
+    // Barrier after "s_waitcnt vmcnt(n) lgkmcnt(0)": n counts the DMA of
+    // later K steps that may stay in flight; vector loads complete in issue
+    // order, so this still waits for the step's own DMA.  The barrier is
+    // written out (no __syncthreads) because its workgroup fence would wait
+    // for every outstanding load; the "memory" clobber keeps the compiler
+    // from moving LDS accesses across it.
     auto sync_vm = [](auto n_c) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(decltype(n_c)::value) : "memory");
     };
-
-    // staged registers: index blk * VEC + k row within the block
-    u32x4 sa_v[(STAGED && !AK) ? NSV : 1], sb_v[(STAGED && !BKM) ? NSV : 1];
 
     // With a transposed-read operand or more than two stages every DMA is
     // issued as inline assembly.  The compiler waits for all LDS DMA in
@@ -259,6 +265,9 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             else if constexpr (ATR)
                 dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * 64], a_tr[trv(n)],
                     (k0 + RPB * (NDMA * wave + n)) * lda * ES);
+            else
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * MNB], a_mnoff,
+                    (k0 + MNR * (NDMA * wave + n)) * lda * ES);
         } else {
             const int m = n - NDMA;
             if constexpr (BKM)
@@ -266,23 +275,10 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             else if constexpr (BTR)
                 dma(false, (lds_ptr_t)&lds[B0 + S * STG + (NDMA * wave + m) * 64], b_tr[trv(m)],
                     (k0 + RPB * (NDMA * wave + m)) * ldb * ES);
+            else
+                dma(false, (lds_ptr_t)&lds[B0 + S * STG + (NDMA * wave + m) * MNB], b_mnoff,
+                    (k0 + MNR * (NDMA * wave + m)) * ldb * ES);
         }
-    };
-    // MN-major staged load v of K step kt (NSV per operand)
-    auto stage_load = [&](int kt, int v) {
-        const int k0 = kt * BK + (v % VEC);
-        const int blk = v / VEC;
-        if constexpr (STAGED && !AK) sa_v[v] = __builtin_amdgcn_raw_buffer_load_b128(ra, mn_off(lda, blk), k0 * lda * ES, 0);
-        if constexpr (STAGED && !BKM) sb_v[v] = __builtin_amdgcn_raw_buffer_load_b128(rb, mn_off(ldb, blk), k0 * ldb * ES, 0);
-    };
-    // MN-major tiles use the swizzle g(r) = (r ^ (r >> 3)) & 7 (swz), which
-    // keeps the transposed writes of lanes on distinct banks.  Row v of the
-    // thread's blocks: block v / VEC, row (mb + 32 blk)*VEC + v % VEC.
-    auto stage_store = [&](int S, int v) {
-        const int blk = v / VEC, i = v % VEC;
-        const int r = (mb + 32 * blk) * VEC + i;
-        if constexpr (STAGED && !AK) lds[A0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sa_v[blk * VEC], i);
-        if constexpr (STAGED && !BKM) lds[B0 + S * STG + r * 8 + swz(r, kb)] = transpose_row<T>(&sb_v[blk * VEC], i);
     };
 
     // ---- MFMA shape --------------------------------------------------------
@@ -291,43 +287,40 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     //   wave's WT x WT block is NF x NF tiles of 16x16 (floatx4).  With random
     //   data gfx950 sustains ~15% more fp16 FLOP/s on 16x16x32 than on
     //   32x32x16 (half the accumulator traffic per FLOP under the power limit).
-    // SH 2, fp32: v_mfma_f32_32x32x2_f32, sub-step s = chunk 4h + s (one MFMA
-    //   per k), NF x NF tiles of 32x32 (4x4 for WT 128, 2x2 for WT 64).
+    // SH 2, fp32: v_mfma_f32_32x32x2_f32, NF x NF tiles of 32x32 (4x4 for WT
+    //   128, 2x2 for WT 64).  In sub-step s lane half h holds k 8s + 4h .. +3
+    //   of its row (a K-major fragment is chunk 2s + h) and MFMA e takes
+    //   element e.
     constexpr int SH = F16 ? 0 : 2;
     constexpr int NSUB = SH == 0 ? 2 : 4;           // sub-steps per K step
     constexpr int UPS = 32 / NSUB;                  // units per sub-step
     constexpr int NF = WT / (SH == 0 ? 16 : 32);    // fragments per operand
     constexpr int MPU = NF * NF / 16;               // MFMAs per unit (SH 0)
     constexpr int FR = SH == 0 ? 16 : 32;           // rows per fragment
-    constexpr int SX = SH == 0 ? 4 : 1;             // sub-step slot offset
+    constexpr int SX = SH == 0 ? 4 : 2;             // sub-step slot offset
     const int fl = SH == 0 ? (lane & 15) : l32;     // fragment row of this lane
-    const int hoff = SH == 0 ? (lane >> 4) : 4 * h; // chunk in sub-step 0
+    const int hoff = SH == 0 ? (lane >> 4) : h;     // chunk in sub-step 0
 
-    // Fragment slot of row r: row base + (hoff ^ g(r)); sub-step s reads it
-    // ^ (s * SX).  Fragment i starts FR rows further on (FR = 16 or 32, a
-    // multiple of 8): its row base moves by the constant ROWSTEP, and g moves
-    // by d(i) = 0 for K-major tiles (g = r & 7) and by ((FR / 8) i) & 7 for
-    // MN-major tiles (g = (r ^ (r >> 3)) & 7: the lane's (r >> 3) & 7 is
-    // fl >> 3 < FR / 8, so adding (FR / 8) i carries into no bit it uses and
-    // acts as an XOR).  The address of fragment i in sub-step s is therefore
-    // base[d(i) ^ s SX] + i ROWSTEP, and i ROWSTEP goes in the ds_read
-    // immediate offset.
-    auto row_base = [&](int r, bool kmajor) { return kmajor ? (r >> 3) * GRP + (r & 7) * 8 : r * 8; };
-    auto gsw = [&](int r, bool kmajor) { return kmajor ? (r & 7) : ((r ^ (r >> 3)) & 7); };
-    constexpr int ASTEP = AK ? (FR / 8) * GRP : FR * 8;
-    constexpr int BSTEP = BKM ? (FR / 8) * GRP : FR * 8;
-    auto dsw = [](bool kmajor, int i) { return kmajor ? 0 : ((FR / 8) * i) & 7; };
+    // K-major fragment slot of row r: row base + (hoff ^ (r & 7)); sub-step s
+    // reads it ^ (s * SX).  Fragment i starts FR rows further on (FR = 16 or
+    // 32, a multiple of 8), which moves the row base by the constant STEP and
+    // leaves r & 7 alone, so STEP i goes in the ds_read immediate offset.
+    auto row_base = [&](int r) { return (r >> 3) * GRP + (r & 7) * 8; };
+    constexpr int STEP = (FR / 8) * GRP;
     int xa[8], xb[8];   // indexed by the slot XOR; unused entries are dead code
     {
         const int ra = wm * WT + fl, rb = wn * WT + fl;
-        const int a0 = row_base(ra, AK), ag = hoff ^ gsw(ra, AK);
-        const int b0 = row_base(rb, BKM), bg = hoff ^ gsw(rb, BKM);
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-            xa[c] = A0 + a0 + (ag ^ c);
-            xb[c] = B0 + b0 + (bg ^ c);
+            xa[c] = A0 + row_base(ra) + ((hoff ^ (ra & 7)) ^ c);
+            xb[c] = B0 + row_base(rb) + ((hoff ^ (rb & 7)) ^ c);
         }
     }
+    // fp32 MN-major fragments: lane (l32, h) reads m = (wave's m) + 32 i + l32
+    // of k row 8 s + 4 h + e for MFMA e: a per-lane byte base with row 4 h;
+    // the k row 8 s + e, fragment i (+128 bytes) and the stage are offsets.
+    const int a_mnb = mn_unit(4 * h) * 16 + (wm * WT + l32) * 4;
+    const int b_mnb = mn_unit(4 * h) * 16 + (wn * WT + l32) * 4;
     // Transposed-read fragments (16-bit MN-major tiles): lane q of group g
     // reads row k = 8g + (q >> 2) at columns 16 i + 4 (q & 3) .. +3 of the
     // wave's WT; its unit is (k / RPB) 64 + (k % RPB) CPR + (c ^ t(k)) with
@@ -383,13 +376,20 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
         dst[2 * half] = w[0];
         dst[2 * half + 1] = w[1];
     };
+    auto mn_frag = [&](u32x4& dst, int byte_off, int s) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            dst[e] = *(lds_u32_t*)((char*)lds + byte_off + mn_unit(8 * s + e) * 16);
+    };
     auto frag_read = [&](int buf, int S, int s, bool isA, int fi, int half) {
         if (isA) {
             if constexpr (ATR) tr_half(af[buf % NAB][fi], half, tra[fi] + S * STG * 16 + s * TR_SUB + half * TR_HALF);
-            else af[buf % NAB][fi] = lds[xa[dsw(AK, fi) ^ (SX * s)] + S * STG + fi * ASTEP];
+            else if constexpr (AMN) mn_frag(af[buf % NAB][fi], (A0 + S * STG) * 16 + a_mnb + 128 * fi, s);
+            else af[buf % NAB][fi] = lds[xa[SX * s] + S * STG + fi * STEP];
         } else {
             if constexpr (BTR) tr_half(bf[buf][fi], half, trb[fi] + S * STG * 16 + s * TR_SUB + half * TR_HALF);
-            else bf[buf][fi] = lds[xb[dsw(BKM, fi) ^ (SX * s)] + S * STG + fi * BSTEP];
+            else if constexpr (BMN) mn_frag(bf[buf][fi], (B0 + S * STG) * 16 + b_mnb + 128 * fi, s);
+            else bf[buf][fi] = lds[xb[SX * s] + S * STG + fi * STEP];
         }
     };
     auto read_one = [&](int buf, int S, int s, int q) {   // the reads of unit q
@@ -432,16 +432,13 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // kt-1 (units [0, UPS), from registers) and the first NSUB-1 sub-steps of
     // kt.  The ND DMA loads of kt+1 are spread over DMA_UNITS units from the
     // first (issued in a burst they oversubscribe the texture address unit
-    // and stall the MFMA issue); staged MN-major rows of kt+1 are written in
-    // units [16, 16 + NSV) and the staged loads of kt+2 issued in [24, 24 +
-    // NSV), after every DMA, which the end-of-region wait relies on.  The first region
-    // has no previous sub-step: its units start at UPS and its DMA is spread
-    // over [UPS, 24).
+    // and stall the MFMA issue).  The first region has no previous sub-step:
+    // its units start at UPS and its DMA is spread over [UPS, 24).
     // 16-bit 256x256 tiles with K-major A and transposed-read B: 24 units
     // (fp16 4096^3 -4%, 8192^3 -1%; the same spread costs the K-major /
     // K-major form 2-3% at 8192^3, and 20 units change neither).
     constexpr int DMA_UNITS = (F16 && WT == 128 && AK && !BKM) ? 24 : VKB_PIPE_DMA_UNITS;
-    static_assert(DMA_UNITS >= 1 && DMA_UNITS <= 24, "the DMA must precede the staged loads of unit 24");
+    static_assert(DMA_UNITS >= 1 && DMA_UNITS <= 24, "DMA spread over 1 .. 24 units");
     auto dma_unit = [&](int kt, int S, int u, bool prev) {   // u: unit of the region
         const int first = prev ? 0 : UPS;
         const int span = prev ? DMA_UNITS : 24 - UPS;
@@ -454,14 +451,14 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // Region, stage S = K step kt:
     //   sub-step NSUB-1 of K step kt-1 (its buffer)  + reads of (kt, 0)
     //   sub-steps 0 .. NSUB-2 of kt                  + reads of the next one
-    //   DMA of kt+1 -> stage S^1; staged rows / loads (see above)
+    //   DMA of kt+1 -> stage S^1
     //   wait for this wave's DMA and LDS traffic, barrier
     // Sub-step s of K step kt uses fragment buffer s & 1 (NSUB is even).
     // Every unit (MFMAs + companions) is fenced with sched_barrier so the
     // compiler keeps this order and both fragment sets live.
     // next: this region issues the DMA of step kt + NST - 1 (into the stage
     // step kt - 1 used); wc: the vmcnt that leaves step kt + 1 landed.
-    auto region = [&](int kt, int S, bool prev, bool next, bool next2, auto wc) {
+    auto region = [&](int kt, int S, bool prev, bool next, auto wc) {
 #pragma unroll
         for (int u = prev ? 0 : UPS; u < 32; ++u) {
             const int sub = u / UPS - 1;          // sub-step of kt run here (-1: kt-1's last)
@@ -470,21 +467,13 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             mfma_unit(buf, q);
             read_one((sub + 1) & 1, S, sub + 1, q);
             if (next) dma_unit(kt + NST - 1, (S + NST - 1) % NST, u, prev);
-            if (STAGED && next && u >= 16 && u < 16 + NSV) stage_store(S ^ 1, u - 16);
-            if (STAGED && next2 && u >= 24 && u < 24 + NSV) stage_load(kt + 2, u - 24);
             __builtin_amdgcn_sched_barrier(0);
         }
         sync_vm(wc);
     };
     using W0 = std::integral_constant<int, 0>;
-    using WS = std::integral_constant<int, NSTAGED>;   // staged loads of kt+2 may still fly
 
-    // ---- prologue: K step 0 into stage 0 (and staged rows of step 1) ----
-    if constexpr (STAGED) {
-        // MN-major first, so waiting for them leaves the direct loads in flight
-#pragma unroll
-        for (int v = 0; v < NSV; ++v) stage_load(0, v);
-    }
+    // ---- prologue: K step 0 into stage 0 (NST 4: steps 1 and 2 too) ----
 #pragma unroll
     for (int n = 0; n < ND; ++n) dma_load(0, 0, n);
     if constexpr (NST == 4) {
@@ -499,13 +488,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             sync_vm(std::integral_constant<int, ND>{});
         }
     } else {
-        if constexpr (STAGED) {
-#pragma unroll
-            for (int v = 0; v < NSV; ++v) stage_store(0, v);
-#pragma unroll
-            for (int v = 0; v < NSV; ++v) stage_load(1, v);   // nkt >= 2
-        }
-        sync_vm(WS{});
+        sync_vm(W0{});
     }
 #pragma unroll
     for (int q = 0; q < UPS; ++q) read_one(0, 0, 0, q);
@@ -516,22 +499,22 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
         using W1 = std::integral_constant<int, ND>;
         using W2 = std::integral_constant<int, 2 * ND>;
         if (nkt == 2) {
-            region(0, 0, false, false, false, W0{});
-            region(1, 1, true, false, false, W0{});
+            region(0, 0, false, false, W0{});
+            region(1, 1, true, false, W0{});
         } else {
-            region(0, 0, false, true, false, W2{});   // loads step 3
+            region(0, 0, false, true, W2{});   // loads step 3
             int kt = 1;
 #pragma clang loop unroll(disable)
-            for (; kt + 3 < nkt; ++kt) region(kt, kt & 3, true, true, false, W2{});
-            region(kt, kt & 3, true, false, false, W1{});             // kt == nkt - 3
-            region(kt + 1, (kt + 1) & 3, true, false, false, W0{});
-            region(kt + 2, (kt + 2) & 3, true, false, false, W0{});
+            for (; kt + 3 < nkt; ++kt) region(kt, kt & 3, true, true, W2{});
+            region(kt, kt & 3, true, false, W1{});             // kt == nkt - 3
+            region(kt + 1, (kt + 1) & 3, true, false, W0{});
+            region(kt + 2, (kt + 2) & 3, true, false, W0{});
         }
     } else if (nkt == 2) {
-        region(0, 0, false, true, false, W0{});
-        region(1, 1, true, false, false, W0{});
+        region(0, 0, false, true, W0{});
+        region(1, 1, true, false, W0{});
     } else {
-        region(0, 0, false, true, true, WS{});
+        region(0, 0, false, true, W0{});
         int kt = 1;
         if constexpr (SH == 0) {
             // One region per iteration, stage from the loop counter: with two
@@ -539,20 +522,20 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             // accumulator tiles different registers in the two halves and
             // copies them around on every iteration (AGPR moves and parking
             // in VGPRs, ~100 extra VALU per two K steps).  The fp32 shape
-            // keeps the constant stages: its staged stores' addresses fold
-            // into immediates, and it shows no such copies.
+            // keeps the constant stages (its LDS addresses fold into
+            // immediates) and shows no such copies.
 #pragma clang loop unroll(disable)
-            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, true, WS{});
-            region(kt, kt & 1, true, true, false, W0{});             // kt == nkt - 2: loads step nkt-1
-            region(kt + 1, (kt + 1) & 1, true, false, false, W0{});
+            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, W0{});
+            region(kt, kt & 1, true, true, W0{});             // kt == nkt - 2: loads step nkt-1
+            region(kt + 1, (kt + 1) & 1, true, false, W0{});
         } else {
             for (; kt + 3 < nkt; kt += 2) {
-                region(kt, 1, true, true, true, WS{});
-                region(kt + 1, 0, true, true, true, WS{});
+                region(kt, 1, true, true, W0{});
+                region(kt + 1, 0, true, true, W0{});
             }
-            region(kt, 1, true, true, true, WS{});       // kt == nkt - 3: stages step nkt-1
-            region(kt + 1, 0, true, true, false, W0{});  // loads step nkt-1
-            region(kt + 2, 1, true, false, false, W0{});
+            region(kt, 1, true, true, W0{});       // kt == nkt - 3
+            region(kt + 1, 0, true, true, W0{});   // loads step nkt-1
+            region(kt + 2, 1, true, false, W0{});
         }
     }
 #pragma unroll
