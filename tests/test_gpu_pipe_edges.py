@@ -157,3 +157,49 @@ def test_pipe_edges_split_k(ab, ct, op_a, op_b):
     assert vk.last_path() == vk.PATH_SPLITK
     # pass 1 on the pipelined kernel (27 workgroups: four stages for 16-bit inputs)
     assert kern == (vk.KERNEL_PIPE128 if ab == "f32" else vk.KERNEL_PIPE128_4), kern
+
+
+@pytest.mark.parametrize("ab,ct", [("f32", "f32"), ("f16", "f16"), ("bf16", "f32")])
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_pipe_edges_strided_batched(ab, ct, op_a, op_b):
+    """a strided batch of ragged matrices on the pipelined 128x128 kernel:
+    every batch's edge tiles shift inside its own matrix (batch strides with
+    a gap between the matrices, which must come back untouched)"""
+    import vkblas_amd as vk
+    from gpu_helpers import normwise, f32_bound, F16_BOUND, BF16_BOUND
+    M, N, K, batch = 296, 264, 256, 3
+    print(f"[case] pipe edges batched {ab}>{ct} op={op_a}{op_b} M={M} N={N} K={K} batch={batch}", flush=True)
+    vk.set_override(1, False)
+    lda = M if op_a else K
+    ldb = K if op_b else N
+    ldc = N
+    sa = lda * (K if op_a else M) + 64
+    sb = ldb * (N if op_b else K) + 64
+    sc = ldc * M + 64
+    ca, ba, tda = _conv(ab)
+    cc, bc, tdc = _conv(ct)
+    a = ca(_uniform(31 + op_a, sa * batch))
+    b = ca(_uniform(33 + op_b, sb * batch))
+    c = cc(_uniform(35, sc * batch))
+    full = c.copy()
+    alpha, beta = 1.25, 0.5
+    fn = {("f32", "f32"): oracle.ref_gemm_f32_rm, ("f16", "f16"): oracle.ref_gemm_f16_rm,
+          ("bf16", "f32"): oracle.ref_gemm_bf16f32_rm}[(ab, ct)]
+    refs = []
+    for i in range(batch):
+        ref = c[i * sc:i * sc + ldc * M].copy()
+        fn(op_a, op_b, M, N, K, a[i * sa:(i + 1) * sa], lda, b[i * sb:(i + 1) * sb], ldb, alpha, beta, ref, ldc)
+        refs.append(ref)
+    dA, dB, dC = _dev(a, tda), _dev(b, tda), _dev(c, tdc)
+    dt = {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}
+    vk.gemm_async(dt[ab], dt[ct], op_a, op_b, M, N, K, alpha, dA.data_ptr(), lda, dB.data_ptr(), ldb, beta,
+                  dC.data_ptr(), ldc, batch=batch, stride_a=sa, stride_b=sb, stride_c=sc, split_k=1)
+    got = _host(dC)
+    # 3 x 9 tiles, fewer workgroups than CUs: four stages for 16-bit inputs, two for fp32
+    assert vk.last_kernel() == (vk.KERNEL_PIPE128 if ab == "f32" else vk.KERNEL_PIPE128_4), vk.last_kernel()
+    bound = f32_bound(K) if ab == "f32" else (BF16_BOUND if ct == "bf16" else F16_BOUND)
+    for i in range(batch):
+        g = got[i * sc:(i + 1) * sc]
+        f = full[i * sc:(i + 1) * sc]
+        assert np.array_equal(g[ldc * M:].view(np.uint8), f[ldc * M:].view(np.uint8))   # gap untouched
+        assert normwise(bc(g[:ldc * M]).astype(np.float64), bc(refs[i]).astype(np.float64)) <= bound
