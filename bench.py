@@ -181,15 +181,16 @@ def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
 
 def shapes(torch, vk, stream, steps):
     """GEMMs off the BASELINE sizes, hipBLAS NN and TN (column-major m x n x
-    k) through the planner: fp32 squares where 128x128 tiles fill the chip
-    (2048^3, 3072^3) or leave no partial wave (5120^3, 6144^3), fp16 3072^3
-    (144 tiles of 256x256), and ragged shapes on the pipelined kernel's
-    shifted edge tiles (m = 4000, a 2047-token fp16 projection)."""
+    k) through the planner: fp32 squares on 128x128 tiles (2048^3 one wave;
+    3072^3 and 5120^3 with a split tail after whole waves; 6144^3), fp16
+    3072^3 (144 tiles of 256x256) and 6144^3 (split tail), and ragged shapes
+    on the pipelined kernel's shifted edge tiles (m = 4000, a 2047-token
+    fp16 projection)."""
     out = {}
     sp = stream.cuda_stream
     cases = [("f32", 2048, 2048, 2048), ("f32", 3072, 3072, 3072), ("f32", 5120, 5120, 5120),
-             ("f32", 6144, 6144, 6144), ("f16", 3072, 3072, 3072), ("f32", 4000, 4000, 4096),
-             ("f16", 4000, 4000, 4096), ("f16", 14336, 2047, 4096)]
+             ("f32", 6144, 6144, 6144), ("f16", 3072, 3072, 3072), ("f16", 6144, 6144, 6144),
+             ("f32", 4000, 4000, 4096), ("f16", 4000, 4000, 4096), ("f16", 14336, 2047, 4096)]
     for dtn, m, n, k in cases:
         g = torch.Generator(device="cuda:0").manual_seed(11)
         A = torch.rand(m * k, device="cuda:0", generator=g) * 2 - 1

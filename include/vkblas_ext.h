@@ -31,7 +31,9 @@ typedef enum {
     VKBLAS_PATH_TILE128 = 2,  /* blocked MFMA GEMM, 128 x 128 tiles        */
     VKBLAS_PATH_TILE256 = 3,  /* blocked MFMA GEMM, 256 x 256 tiles        */
     VKBLAS_PATH_SPLITK = 4,   /* split-K pass 1 + deterministic reduce     */
-    VKBLAS_PATH_SKINNY = 5    /* bandwidth-bound skinny fp16 (M <= 16)     */
+    VKBLAS_PATH_SKINNY = 5,   /* bandwidth-bound decode (M <= 64)          */
+    VKBLAS_PATH_TAIL = 6      /* whole waves of tiles, then split-K over
+                                 the last tail_rows rows of C             */
 } vkblas_path_t;
 
 /* GEMM kernel that ran (vkblas_last_kernel); the values equal the
@@ -49,8 +51,12 @@ typedef enum {
 typedef struct {
     int path;              /* vkblas_path_t                                 */
     int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256)  */
-    uint32_t split;        /* split-K factor, 1 = no split                  */
+    uint32_t split;        /* split-K factor, 1 = no split (VKBLAS_PATH_TAIL:
+                              the split of the tail rows)                  */
     uint32_t k_per_split;  /* K per split (multiple of the tile's K step)   */
+    uint32_t tail_rows;    /* VKBLAS_PATH_TAIL: rows M - tail_rows .. M - 1
+                              run split-K, the rows before them as tiles;
+                              0 otherwise                                  */
 } vkblas_plan_t;
 
 /*

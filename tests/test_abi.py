@@ -176,12 +176,37 @@ def test_plan_headline_configs():
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 512, 512, 512, 512, 512, 512, batch=64).split == 1
 
 
+def test_plan_split_tail():
+    """A partial last wave (at most half full) after whole waves of tiles:
+    the last tile rows run split-K with as many slices as fit in one wave."""
+    def pl(dt, M, N, K, **kw):
+        return P(dt, dt, 0, 0, M, N, K, K, N, N, **kw)
+    p = pl(vk.DT_F32, 3072, 3072, 3072)      # 24 x 24 tiles of 128: 512 + 64
+    assert (p.path, p.tile, p.tail_rows, p.split, p.k_per_split) == (vk.PATH_TAIL, 1, 384, 7, 448)
+    p = pl(vk.DT_F32, 5120, 5120, 5120)      # 40 x 40: 3 x 512 + 64
+    assert (p.path, p.tail_rows, p.split) == (vk.PATH_TAIL, 256, 6)
+    p = pl(vk.DT_F16, 6144, 6144, 6144)      # 24 x 24 tiles of 256: 2 x 256 + 64
+    assert (p.path, p.tile, p.tail_rows, p.split) == (vk.PATH_TAIL, 2, 768, 3)
+    p = pl(vk.DT_F32, 3000, 3072, 1024)      # ragged M: the tail holds the partial tile row
+    assert (p.path, p.tail_rows) == (vk.PATH_TAIL, 3000 - 21 * 128)
+    assert p.split * p.k_per_split >= 1024 > (p.split - 1) * p.k_per_split and p.k_per_split % 64 == 0
+    # whole waves, a last wave more than half full, or under one wave: tiles only
+    for dt, n in ((vk.DT_F32, 4096), (vk.DT_F32, 2048), (vk.DT_F16, 5120), (vk.DT_F16, 4096), (vk.DT_F32, 6144)):
+        p = pl(dt, n, n, n)
+        assert p.path in (vk.PATH_TILE128, vk.PATH_TILE256) and p.tail_rows == 0 and p.split == 1
+    # a caller's split, never-split, batches and unaligned operands keep their plans
+    assert pl(vk.DT_F32, 3072, 3072, 3072, split_k=1).path == vk.PATH_TILE128
+    assert pl(vk.DT_F32, 3072, 3072, 3072, split_k=4).path == vk.PATH_SPLITK
+    assert pl(vk.DT_F32, 3072, 3072, 3072, batch=2).path == vk.PATH_TILE128
+    assert pl(vk.DT_F32, 3072, 3072, 3072, aligned=False).path != vk.PATH_TAIL
+
+
 def test_plan_tile_crossover():
     """Square shapes where both pipelined tile sizes apply: fp32 keeps
     256x256 tiles only for about whole waves of one workgroup per CU; 16-bit
     inputs take them from 128 tiles on."""
     def tile(dt, n, batch=1):
-        pl = P(dt, dt, 0, 0, n, n, n, n, n, n, batch=batch)
+        pl = P(dt, dt, 0, 0, n, n, n, n, n, n, batch=batch, split_k=1)   # no split tail
         assert pl.split == 1
         return pl.path
     T128, T256 = vk.PATH_TILE128, vk.PATH_TILE256

@@ -35,8 +35,8 @@ DT_F32, DT_F16, DT_BF16 = 0, 1, 2
 # vkblas_scalar_mode_t
 SCALAR_HOST, SCALAR_DEV_F32, SCALAR_DEV_F16 = 0, 1, 2
 # vkblas_path_t
-PATH_NONE, PATH_TILE64, PATH_TILE128, PATH_TILE256, PATH_SPLITK, PATH_SKINNY = range(6)
-PATH_NAMES = {0: "none", 1: "tile64", 2: "tile128", 3: "tile256", 4: "splitk", 5: "skinny"}
+PATH_NONE, PATH_TILE64, PATH_TILE128, PATH_TILE256, PATH_SPLITK, PATH_SKINNY, PATH_TAIL = range(7)
+PATH_NAMES = {0: "none", 1: "tile64", 2: "tile128", 3: "tile256", 4: "splitk", 5: "skinny", 6: "tail"}
 
 
 class VkblasError(RuntimeError):
@@ -53,7 +53,7 @@ class Epilogue(ctypes.Structure):
 
 class Plan(ctypes.Structure):
     _fields_ = [("path", ctypes.c_int), ("tile", ctypes.c_int), ("split", ctypes.c_uint32),
-                ("k_per_split", ctypes.c_uint32)]
+                ("k_per_split", ctypes.c_uint32), ("tail_rows", ctypes.c_uint32)]
 
 
 _lib = None

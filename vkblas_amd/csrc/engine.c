@@ -461,6 +461,41 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             return VKBLAS_OK;
         }
     }
+    /* A partial last wave: with T tiles on `slots` concurrent workgroups
+     * (one 256x256 or two 128x128 per CU on 256 CUs), T = W slots + R and
+     * R at most half a wave leaves most CUs idle for a whole tile time.
+     * The rows of the first tiles_m - r tile rows then run as tiles (W
+     * waves, a few slots idle) and the last r rows (the R tiles rounded up
+     * to whole rows) as split-K with as many slices as fit in one wave,
+     * pass 1 on the same pipelined tile.  Measured (one box): fp32 3072^3
+     * on 128x128 tiles 509.0 -> 411.3 us (7 slices of 3 tile rows; 4 / 8
+     * slices 439.9 / 428.1), fp32 5120^3 1991.7 -> 1819.2 us (6 slices of
+     * 2 rows). */
+    if (split_k == 0 && batch == 1 && (tile == VKB_TILE_128 || tile == VKB_TILE_256) &&
+        pipe_ok(ab_type, tile, op_a, op_b, M, N, K, lda, ldb, aligned)) {
+        const uint32_t edge = vkb_tile_bm(tile);
+        const uint64_t slots = tile == VKB_TILE_256 ? 256 : 512;
+        const uint64_t tm = cdiv(M, edge), tn = cdiv(N, edge), T = tm * tn;
+        const uint64_t W = T / slots, R = T % slots;
+        if (W >= 1 && R > 0 && 2 * R <= slots) {
+            const uint64_t rows_t = (R + tn - 1) / tn;            /* tail tile rows */
+            const uint32_t head = (uint32_t)((tm - rows_t) * edge);
+            const uint32_t tail = M - head;
+            uint64_t s = slots / (rows_t * tn);
+            const uint64_t kmax = K / (PIPE_MIN_STEPS * bk);
+            if (s > kmax) s = kmax;
+            const uint32_t kpair = 2 * bk;
+            if (s >= 2 && tail >= edge && s * tail * (uint64_t)N * 4 <= (1ull << 30)) {
+                const uint32_t kps = cdiv(cdiv(K, s), kpair) * kpair;
+                plan->path = VKBLAS_PATH_TAIL;
+                plan->tile = tile;
+                plan->split = cdiv(K, kps);
+                plan->k_per_split = kps;
+                plan->tail_rows = tail;
+                return VKBLAS_OK;
+            }
+        }
+    }
     plan->path = tile_path(tile);
     plan->tile = tile;
     plan->split = 1;
@@ -477,6 +512,7 @@ static const char* path_name(int p) {
         case VKBLAS_PATH_TILE256: return "tile256";
         case VKBLAS_PATH_SPLITK: return "splitk";
         case VKBLAS_PATH_SKINNY: return "skinny";
+        case VKBLAS_PATH_TAIL: return "tail";
         default: return "none";
     }
 }
@@ -570,9 +606,12 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
                 op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
                 path_name(plan.path), plan.split, ws_ext ? " (scratch)" : "");
 
-    /* partials: [split][M][N] fp32 for split-K and the split decode kernel */
-    const int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK);
-    const size_t ws_bytes = partials ? (size_t)plan.split * M * N * sizeof(float) : 0;
+    /* partials: [split][M][N] fp32 for split-K and the split decode kernel,
+     * [split][tail_rows][N] for the split tail */
+    const int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK ||
+                                            plan.path == VKBLAS_PATH_TAIL);
+    const uint32_t prow = plan.path == VKBLAS_PATH_TAIL ? plan.tail_rows : M;   /* rows of the partials */
+    const size_t ws_bytes = partials ? (size_t)plan.split * prow * N * sizeof(float) : 0;
     if (ws_ext && ws_bytes > ws_ext_bytes) {
         if (g_trace)
             fprintf(stderr, "[vkblas] partials of %zu bytes exceed the %zu-byte scratch buffer\n", ws_bytes,
@@ -621,7 +660,41 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
         a.generic_only = g_generic_only;
         a.kernel_out = &kernel;
         a.epi = epp;
-        if (plan.path == VKBLAS_PATH_SPLITK) {
+        if (plan.path == VKBLAS_PATH_TAIL) {
+            /* rows [0, head) as tiles, rows [head, M) split-K into the
+             * workspace and reduced into C with the epilogue; batch == 1 */
+            const uint32_t head = M - plan.tail_rows;
+            const size_t es_ab = ab == VKB_T_F32 ? 4 : 2, es_c = ct == VKB_T_F32 ? 4 : 2;
+            a.M = head;
+            rc = vkb_launch_gemm(&a, plan.tile, stream);
+            vkb_gemm_args t = a;
+            t.M = plan.tail_rows;
+            t.A = (const char*)A + (size_t)head * (op_a == VKBLAS_OP_N ? (size_t)lda : 1) * es_ab;
+            t.C = ws;
+            t.ldc = N;
+            t.c_type = VKB_T_F32;
+            t.split = plan.split;
+            t.k_per_split = plan.k_per_split;
+            t.stride_split = (int64_t)plan.tail_rows * N;
+            t.alpha = 1.0f; t.beta = 0.0f;
+            t.scalar_mode = VKB_SCALAR_HOST;
+            t.alpha_dev = t.beta_dev = NULL;
+            t.epi = NULL;
+            int tail_kernel = 0;
+            t.kernel_out = &tail_kernel;
+            if (rc == 0) rc = vkb_launch_gemm(&t, plan.tile, stream);
+            vkb_epilogue_args tep;
+            memset(&tep, 0, sizeof(tep));
+            if (epp) {
+                tep = *epp;
+                if (tep.c_in) tep.c_in = (const char*)tep.c_in + (size_t)head * tep.ldc_in * es_c;
+            }
+            if (rc == 0)
+                rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)plan.tail_rows * N, plan.split,
+                                              plan.tail_rows, N, (char*)C + (size_t)head * ldc * es_c, ldc, ct,
+                                              alpha, beta, (int)scalar_mode, alpha_dev, beta_dev,
+                                              epp ? &tep : NULL, stream);
+        } else if (plan.path == VKBLAS_PATH_SPLITK) {
             a.C = ws;
             a.ldc = N;
             a.stride_c = 0;
