@@ -218,3 +218,49 @@ def test_workspace_release_then_reuse():
     assert np.array_equal(_bits(c1), want)
     vk.workspace_release()
     vk.workspace_release()
+
+
+CHILD_NO_ROOM = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+import oracle, vkblas_amd as vk
+from gpu_helpers import normwise, f32_bound
+M = N = 1024; K = 8192
+rng = np.random.default_rng(5)
+a = rng.uniform(-1, 1, M * K).astype(np.float32); b = rng.uniform(-1, 1, K * N).astype(np.float32)
+dA, dB = torch.from_numpy(a).cuda(), torch.from_numpy(b).cuda()
+pl = vk.plan(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, K, N, N)
+assert pl.path == vk.PATH_SPLITK and pl.split == 128, (pl.path, pl.split)
+assert pl.split * M * N * 4 > vk.noalloc_scratch_bytes()
+rows = oracle.sample_rows(M, 12)
+ref = np.zeros(M * N, np.float32)
+oracle.ref_gemm_f32_rm(0, 0, M, N, K, a, K, b, N, 1.0, 0.0, ref, N, rows=rows)
+for name in ("noalloc", "async"):
+    dC = torch.full((M * N,), float("nan"), device="cuda:0")
+    fn = vk.gemm_noalloc_async if name == "noalloc" else vk.gemm_async
+    fn(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(), N, 0.0, dC.data_ptr(), N)
+    path = vk.last_path()
+    # the scratch has no room for 128 slices: the heuristic split falls back
+    # to the plan without a split; the workspace path keeps the split
+    assert path == (vk.PATH_TILE128 if name == "noalloc" else vk.PATH_SPLITK), (name, path)
+    got = dC.cpu().numpy().reshape(M, N)[rows]
+    assert normwise(got, ref.reshape(M, N)[rows]) <= f32_bound(K), name
+print("NO ROOM OK")
+"""
+
+
+def test_heuristic_split_without_room_runs_unsplit(tmp_path):
+    """A planner-chosen split (here VKBLAS_SPLITK=128, which sets the
+    heuristic's split) whose partials exceed the no-alloc scratch runs
+    without a split instead of failing; a caller's split_k > 1 is still
+    rejected (test_zz_no_alloc).  Runs in a child process: VKBLAS_SPLITK is
+    read once per process."""
+    import os
+    import subprocess
+    import sys
+    print("[case] heuristic split without room for the partials", flush=True)
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, VKBLAS_SPLITK="128", PYTHONPATH=os.path.join(repo, "tests") + os.pathsep + repo)
+    r = subprocess.run([sys.executable, "-c", CHILD_NO_ROOM, repo], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "NO ROOM OK" in r.stdout, f"rc={r.returncode}\n{r.stdout[-3000:]}\n{r.stderr[-3000:]}"

@@ -608,28 +608,47 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
 
     /* partials: [split][M][N] fp32 for split-K and the split decode kernel,
      * [split][tail_rows][N] for the split tail */
-    const int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK ||
-                                            plan.path == VKBLAS_PATH_TAIL);
-    const uint32_t prow = plan.path == VKBLAS_PATH_TAIL ? plan.tail_rows : M;   /* rows of the partials */
-    const size_t ws_bytes = partials ? (size_t)plan.split * prow * N * sizeof(float) : 0;
-    if (ws_ext && ws_bytes > ws_ext_bytes) {
-        if (g_trace)
-            fprintf(stderr, "[vkblas] partials of %zu bytes exceed the %zu-byte scratch buffer\n", ws_bytes,
-                    ws_ext_bytes);
-        return VKBLAS_ERR_PARAM;
-    }
+    int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK ||
+                                      plan.path == VKBLAS_PATH_TAIL);
+    size_t ws_bytes = partials ? (size_t)plan.split * (plan.path == VKBLAS_PATH_TAIL ? plan.tail_rows : M) * N *
+                                     sizeof(float)
+                               : 0;
+    /* The planner's own K splits (split-K for few output tiles, the split
+     * tail) only speed a call up: where their partials have no room (the
+     * caller's scratch is smaller; a capturing stream declines the
+     * workspace) the call runs the plan without a split instead of failing.
+     * A caller's split (split_k > 1) and the decode kernels' splits keep
+     * their plan and fail. */
+    const int optional = split_k == 0 && (plan.path == VKBLAS_PATH_SPLITK || plan.path == VKBLAS_PATH_TAIL);
     prof_t pf;
     if (!ws_ext) prof_begin(&pf, hs);
     else memset(&pf, 0, sizeof(pf));
     ws_lease_t lease = {NULL, -1, 0, hs};
     void* ws = ws_ext;
+    int room = 1;
+    if (partials && ws_ext) room = ws_bytes <= ws_ext_bytes;
     if (partials && !ws_ext) {
-        if (ws_acquire(hs, ws_bytes, &lease) != 0) {
-            ws_release(&lease);
-            prof_end(&pf, hs, "gemm", 0);
-            return VKBLAS_ERR_INIT;
-        }
+        room = ws_acquire(hs, ws_bytes, &lease) == 0;
+        if (!room) ws_release(&lease);
         ws = lease.ptr;
+    }
+    if (!room && optional &&
+        vkblas_plan_gemm(ab_type, c_type, op_a, op_b, M, N, K, lda, ldb, ldc, batch, 1, aligned, &plan) ==
+            VKBLAS_OK &&
+        plan.split == 1) {
+        if (g_trace) fprintf(stderr, "[vkblas] no room for the partials: plan without a split (%s)\n",
+                             path_name(plan.path));
+        partials = 0;
+        ws_bytes = 0;
+        room = 1;
+        ws = NULL;
+    }
+    if (!room) {
+        if (g_trace && ws_ext)
+            fprintf(stderr, "[vkblas] partials of %zu bytes exceed the %zu-byte scratch buffer\n", ws_bytes,
+                    ws_ext_bytes);
+        prof_end(&pf, hs, "gemm", 0);
+        return ws_ext ? VKBLAS_ERR_PARAM : VKBLAS_ERR_INIT;
     }
 
     if (plan.path == VKBLAS_PATH_SKINNY) {
