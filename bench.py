@@ -507,9 +507,10 @@ def splitk(torch, vk, stream, steps, splits=(4, 16, 64, 0)):
 def vendor(torch, vk, stream, steps):
     """The same workloads through PyTorch's own GEMM backend (hipBLASLt on
     gfx950), timed like the vkblas legs: fp32 / fp16 / bf16 4096^3 (row-major
-    a @ b and a @ b.t(), i.e. hipBLAS NN and TN) and 8192x8192 fp16 decode
-    x @ w.t() with three weight copies rotated.  Not part of the default run:
-    the comparison in DESIGN.md comes from here."""
+    a @ b and a @ b.t(), i.e. hipBLAS NN and TN), the `shapes` leg's GEMMs
+    (a @ b) and 8192x8192 fp16 decode x @ w.t() with three weight copies
+    rotated.  Not part of the default run: the comparison in DESIGN.md comes
+    from here (plain, and with libvkblas_hipblas.so under LD_PRELOAD)."""
     n = 4096
     g = torch.Generator(device="cuda:0").manual_seed(7)
     out = {}
@@ -521,6 +522,19 @@ def vendor(torch, vk, stream, steps):
             warm(torch, lambda i: f())
             med = batch_ms(torch, stream, lambda i: f(), max(steps, 20))
             out[f"{name}_{n}_{lay}"] = {"ms": round(med, 4), "tflops": round(2.0 * n ** 3 / (med * 1e-3) / 1e12, 1)}
+    # the shapes of the `shapes` leg, row-major a @ b (hipBLAS NN)
+    for name, dt, m, nn, k in (("fp32_3072", torch.float32, 3072, 3072, 3072),
+                               ("fp32_5120", torch.float32, 5120, 5120, 5120),
+                               ("fp32_4000x4000x4096", torch.float32, 4000, 4000, 4096),
+                               ("fp16_3072", torch.float16, 3072, 3072, 3072),
+                               ("fp16_6144", torch.float16, 6144, 6144, 6144),
+                               ("fp16_2047x14336x4096", torch.float16, 2047, 14336, 4096)):
+        a = (torch.randn(m, k, device="cuda:0", generator=g) / math.sqrt(k)).to(dt)
+        b = (torch.randn(k, nn, device="cuda:0", generator=g) / math.sqrt(k)).to(dt)
+        warm(torch, lambda i: a @ b)
+        med = batch_ms(torch, stream, lambda i: a @ b, max(steps, 10))
+        out[f"{name}_NN"] = {"ms": round(med, 4), "tflops": round(2.0 * m * nn * k / (med * 1e-3) / 1e12, 1)}
+        del a, b
     K = O = 8192
     Ws = [(torch.randn(O, K, device="cuda:0", generator=g) * 0.02).half() for _ in range(3)]
     X = torch.randn(64, K, device="cuda:0", generator=g).half()
