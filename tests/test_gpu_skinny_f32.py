@@ -55,6 +55,10 @@ CASES_N += [
     (16, 4096, 14336, 0, 0, 0, 0.0),     # K split 32 ways
     (9, 1024, 65536, 4, 4, 2, 0.25),     # split, ragged everything else
     (1, 8192, 8192, 0, 0, 0, 0.0),       # the bench shape
+    (4, 2048, 8200, 4, 8, 0, 0.0),       # split, the last slice ending in a partial chunk
+    (16, 260, 33, 3, 4, 4, 0.5),         # two full chunks and a 1-row partial one
+    (5, 516, 20, 0, 0, 0, -0.5),         # one full chunk and a partial one; 5 column blocks
+    (8, 252, 4096, 0, 4, 0, 0.0),        # the second 128-column block partial
 ]
 
 
