@@ -216,10 +216,11 @@ def shapes(torch, vk, stream, steps):
     return out
 
 
-def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=False):
+def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=False, kxo=False):
     """configs[3]: decode GemmEx(T, N, m=O, n=ntok, k=K), W K-contiguous;
     three weight copies (3 x 128 MiB > 256 MB MALL) rotated per launch
-    (bf16: the same with 16BF data)."""
+    (bf16: the same with 16BF data; kxo: the weight stored K x O instead,
+    GemmEx(N, N), PyTorch's x @ w)."""
     dt = torch.bfloat16 if bf16 else torch.float16
     vdt = vk.DT_BF16 if bf16 else vk.DT_F16
     g = torch.Generator(device="cuda:0").manual_seed(11)
@@ -230,8 +231,8 @@ def matvec(torch, vk, stream, steps, K=8192, O=8192, ntoks=(1, 4, 8, 16), bf16=F
     out = {}
     for nt in ntoks:
         def call(i):
-            vk.gemm_async(vdt, vdt, vk.OP_N, vk.OP_T, nt, O, K, 1.0, X.data_ptr(), K,
-                          Ws[i % 3].data_ptr(), K, 0.0, Y.data_ptr(), O, stream=sp)
+            vk.gemm_async(vdt, vdt, vk.OP_N, vk.OP_N if kxo else vk.OP_T, nt, O, K, 1.0, X.data_ptr(), K,
+                          Ws[i % 3].data_ptr(), O if kxo else K, 0.0, Y.data_ptr(), O, stream=sp)
         warm(torch, call)
         med = batch_ms(torch, stream, call, 3 * max(steps, 10))
         nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
@@ -357,7 +358,8 @@ def main():
         return
     if args.only == "matvec":
         print(json.dumps({"n1-16": matvec(torch, vk, stream, args.steps),
-                          "n24-64": matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))}))
+                          "n24-64": matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64)),
+                          "KxO_n1-16": matvec(torch, vk, stream, args.steps, kxo=True)}))
         return
     if args.only == "matvec_ns":
         print(json.dumps({"4096x14336": matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 4, 8, 12, 16)),
@@ -441,6 +443,8 @@ def main():
     line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 4, 8, 16))
     log("[bench] decode 8192x8192, 24-64 tokens")
     line["fp16_decode_8192_wide"] = matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))
+    log("[bench] fp16 matvec 8192x8192, weight stored K x O")
+    line["fp16_matvec_8192_KxO"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8, 16), kxo=True)
     log("[bench] fp32 matvec 8192x8192, both weight layouts")
     line["fp32_matvec_8192"] = matvec_f32(torch, vk, stream, args.steps)
     log("[bench] split-K and strided-batched")

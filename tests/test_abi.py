@@ -275,6 +275,29 @@ def test_plan_skinny_f32():
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 4096, 4096, 4096, 1 << 30, 4096).path == vk.PATH_SKINNY
 
 
+def test_plan_skinny_16bit_kn():
+    """fp16 / bf16 with up to 16 activation rows and the weight stored K x N
+    (op_b = N, PyTorch's x @ w): the 16-bit K x N kernel, N a multiple of 8,
+    K split in 64-row groups so that the grid holds at most 256 workgroups of
+    256 columns, each slice at least 4 groups."""
+    for dt in (vk.DT_F16, vk.DT_BF16):
+        for M in (1, 4, 16):
+            pl = P(dt, dt, 0, 0, M, 8192, 8192, 8192, 8192, 8192)
+            assert pl.path == vk.PATH_SKINNY and pl.split == 8     # 32 column blocks x 8 slices
+        assert P(dt, vk.DT_F32, 0, 0, 3, 2048, 65536, 65536, 2048, 2048).split == 32
+        assert P(dt, dt, 0, 0, 1, 14336, 4096, 4096, 14336, 14336).split == 4
+        assert P(dt, dt, 0, 0, 16, 4096, 14336, 14336, 4096, 4096).split == 16
+        assert P(dt, dt, 0, 0, 4, 8, 32, 32, 8, 8).split == 1
+    # not this kernel: 17 rows, N % 8, ldb % 8, ldb short of N, lda % 8 (M > 1)
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8188, 8192, 8192, 8192, 8188).path != vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8192, 8192, 8192, 8196, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8192, 8192, 8192, 8184, 8192).path != vk.PATH_SKINNY
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8192, 8192, 8196, 8192, 8192).path != vk.PATH_SKINNY
+    # one activation row: its leading dimension is never used
+    assert P(vk.DT_BF16, vk.DT_BF16, 0, 0, 1, 8192, 8192, 3, 8192, 8192).path == vk.PATH_SKINNY
+
+
 def test_plan_decode_span_limit():
     """The decode kernels address a 32-row weight tile and the activation
     rows with 32-bit buffer offsets; a decode-shaped call whose leading

@@ -121,11 +121,14 @@ def _mark_skinny(vk, skinny=True):
     """an engine call whose path a case does not take (the decode kernels, or
     with skinny=False a 64x64 tile): a forwarded call leaves that path as
     vkblas_last_path"""
-    x = torch.zeros(2 * 64, dtype=torch.float16, device="cuda:0")
+    # 2 rows against W stored N x K: the decode kernels; 17 rows against W
+    # stored K x N (more than its decode kernel takes): a 64x64 tile
+    rows = 2 if skinny else 17
+    x = torch.zeros(rows * 64, dtype=torch.float16, device="cuda:0")
     w = torch.zeros(64 * 64, dtype=torch.float16, device="cuda:0")
-    y = torch.zeros(2 * 64, dtype=torch.float16, device="cuda:0")
-    vk.gemm_async(vk.DT_F16, vk.DT_F16, 0, 1 if skinny else 0, 2, 64, 64, 1.0, x.data_ptr(), 64, w.data_ptr(), 64,
-                  0.0, y.data_ptr(), 64)
+    y = torch.zeros(rows * 64, dtype=torch.float16, device="cuda:0")
+    vk.gemm_async(vk.DT_F16, vk.DT_F16, 0, 1 if skinny else 0, rows, 64, 64, 1.0, x.data_ptr(), 64, w.data_ptr(),
+                  64, 0.0, y.data_ptr(), 64)
     torch.cuda.synchronize()
     assert vk.last_path() == (vk.PATH_SKINNY if skinny else vk.PATH_TILE64)
     return vk.last_path()

@@ -1,6 +1,7 @@
 """Edge cases of the decode kernels (engine op_a = N, op_b = T, M <= 64: the
 GEMV kernel for M <= 2, the MFMA skinny kernel above, with up to four
-16-row activation tiles from M = 17; fp16 and bf16), the path the
+16-row activation tiles from M = 17; op_b = N, M <= 16: the K x N kernel;
+fp16 and bf16), the path the
 reference reaches for matvec / skinny shapes (src/vkblas.c:2100-2392,
 2501-2808).  Ragged K (not a multiple of the kernels' K steps), padded
 leading dimensions whose padding holds NaN (it must never reach C), beta != 0,
@@ -178,5 +179,107 @@ def test_decode_deterministic():
             dC = torch.empty(M * N, dtype=torch.float16, device="cuda:0")
             vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_T, M, N, K, 1.0, dX.data_ptr(), K, dW.data_ptr(), K,
                           0.0, dC.data_ptr(), N, stream=torch.cuda.current_stream().cuda_stream)
+            outs.append(to_host(dC))
+        assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+# Weight stored K x N (engine op_b = N, PyTorch's x @ w): the 16-bit K x N
+# kernel for up to 16 activation rows, N a multiple of 8.  (M, N, K, pad_a,
+# pad_b, beta, out): ldb = N + pad_b with NaN in the padding columns; ragged K
+# (not a multiple of the 32-row chunk), N not a multiple of the workgroup's
+# 256 columns, K split over the grid with fp32 partials and the reduce.
+CASES_KN = []
+for M in (1, 2, 5, 8, 16):
+    for (N, K) in ((8, 32), (264, 1000), (1000, 1032), (4096, 4100)):
+        CASES_KN.append((M, N, K, -K % 8, 0, 0.0, "f16"))   # lda a multiple of 8
+CASES_KN += [
+    (1, 8192, 8192, 0, 0, 0.0, "f16"),       # the bench shape, K split 8 ways
+    (16, 8192, 8192, 0, 8, 0.5, "bf16"),
+    (3, 2048, 65536, 8, 16, 0.0, "f16>f32"),  # 32 slices
+    (9, 520, 33, 7, 8, -0.5, "bf16>f32"),    # one full chunk and one row
+    (4, 776, 7, 1, 0, 0.25, "f16"),           # a partial chunk only
+    (12, 1032, 2056, 8, 24, 1.0, "bf16"),
+    (2, 8, 4104, 0, 8, 0.0, "f32"),
+]
+
+
+@pytest.mark.parametrize("case", CASES_KN, ids=lambda c: f"M{c[0]}_N{c[1]}_K{c[2]}_pa{c[3]}_pb{c[4]}_b{c[5]}_{c[6]}")
+def test_decode_kn(case):
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND, BF16_BOUND
+    M, N, K, pad_a, pad_b, beta, out = case
+    print(f"[case] decode K x N {case}", flush=True)
+    bf = out.startswith("bf16")
+    f32 = out.endswith("f32")
+    lda, ldb, ldc = K + pad_a, N + pad_b, N
+    hX = _padded(M, K, lda, 5 + M + K, 1.0, bf)
+    hW = _padded(K, N, ldb, 6 + N + K, 0.05, bf)
+    r = np.random.default_rng(7)
+    c = r.standard_normal(M * ldc).astype(np.float32)
+    hC = c if f32 else (oracle.f2bf_rne(c) if bf else oracle.f2h_rne(c))
+    want = hC.copy()
+    if bf:
+        ref = oracle.ref_gemm_bf16f32_rm if f32 else oracle.ref_gemm_bf16_rm
+    else:
+        ref = oracle.ref_gemm_f16f32_rm if f32 else oracle.ref_gemm_f16_rm
+    ref(0, 0, M, N, K, hX, lda, hW, ldb, 1.5, beta, want, ldc)
+    dX, dW, dC = to_dev(hX), to_dev(hW), to_dev(hC)
+    ab = vk.DT_BF16 if bf else vk.DT_F16
+    pl = vk.plan(ab, vk.DT_F32 if f32 else ab, 0, 0, M, N, K, lda, ldb, ldc)
+    assert pl.path == vk.PATH_SKINNY, pl.path
+    vk.gemm_async(ab, vk.DT_F32 if f32 else ab, vk.OP_N, vk.OP_N, M, N, K, 1.5, dX.data_ptr(), lda,
+                  dW.data_ptr(), ldb, beta, dC.data_ptr(), ldc, stream=torch.cuda.current_stream().cuda_stream)
+    assert vk.last_path() == vk.PATH_SKINNY
+    got = to_host(dC)
+    if f32:
+        g, w = got, want
+    else:
+        dec = oracle.bf2f if bf else oracle.h2f
+        g, w = dec(got), dec(want)
+    assert np.all(np.isfinite(g))
+    assert normwise(g, w) <= (BF16_BOUND if bf and not f32 else F16_BOUND)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 1032), (7, 8192, 8192)])
+@pytest.mark.parametrize("sep", [False, True])
+def test_decode_kn_epilogue(M, N, K, sep):
+    """bias and a separate C input on the K x N kernel: in its own epilogue,
+    or once in the reduce after a K split (8192 x 8192)"""
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host, normwise, F16_BOUND
+    print(f"[case] decode K x N epilogue M={M} N={N} K={K} sep={sep}", flush=True)
+    hX = _padded(M, K, K, 31, 1.0)
+    hW = _padded(K, N, N, 32, 0.05)
+    r = np.random.default_rng(33)
+    hC = oracle.f2h_rne(r.standard_normal(M * N).astype(np.float32))
+    cin = oracle.f2h_rne(r.standard_normal(M * N).astype(np.float32))
+    bias = (r.standard_normal(N) * 0.5).astype(np.float32)
+    want = hC.copy()
+    oracle.ref_gemm_epi_rm("f16", "f16", 0, 0, M, N, K, hX, K, hW, N, 1.25, -0.5,
+                           cin if sep else want.copy(), N, want, N, bias)
+    dX, dW, dC, dCin, dB = to_dev(hX), to_dev(hW), to_dev(hC), to_dev(cin), to_dev(bias)
+    vk.gemm_ex_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_N, M, N, K, 1.25, dX.data_ptr(), K, dW.data_ptr(), N,
+                     -0.5, dC.data_ptr(), N, c_in=dCin.data_ptr() if sep else None, ldc_in=N if sep else 0,
+                     bias=dB.data_ptr(), bias_type=vk.DT_F32, stream=torch.cuda.current_stream().cuda_stream)
+    assert vk.last_path() == vk.PATH_SKINNY
+    assert normwise(oracle.h2f(to_host(dC)), oracle.h2f(want)) <= F16_BOUND
+
+
+def test_decode_kn_deterministic():
+    """K x N kernel and its K split: repeated runs are bitwise equal"""
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import to_dev, to_host
+    print("[case] decode K x N determinism", flush=True)
+    for M, N, K in ((1, 8192, 8192), (16, 4096, 14336), (5, 1000, 1032)):
+        dX, dW = to_dev(_padded(M, K, K, 41, 1.0)), to_dev(_padded(K, N, N, 42, 0.05))
+        outs = []
+        for _ in range(3):
+            dC = torch.empty(M * N, dtype=torch.float16, device="cuda:0")
+            vk.gemm_async(vk.DT_F16, vk.DT_F16, vk.OP_N, vk.OP_N, M, N, K, 1.0, dX.data_ptr(), K, dW.data_ptr(), N,
+                          0.0, dC.data_ptr(), N, stream=torch.cuda.current_stream().cuda_stream)
+            assert vk.last_path() == vk.PATH_SKINNY
             outs.append(to_host(dC))
         assert all(np.array_equal(outs[0], o) for o in outs[1:])

@@ -804,6 +804,147 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
     }
 }
 
+// 16-bit form of the N-contiguous decode (weight K x N, engine op_b = N:
+// PyTorch's x @ w with w stored [K][N]).  One v_mfma_f32_16x16x32 takes 8 k
+// of 16 activation rows (A: lane (l16, g) holds X[l16][k0 + 8 g .. + 7], one
+// 16-byte load) against the same 8 k of 16 columns (B: lane (l16, g) holds
+// W[k0 + 8 g .. + 7][column of lane l16]).  A lane loads 16 bytes (columns
+// nl .. nl + 7, nl = n0 + 8 l16) of each of its 8 k rows, so a load
+// instruction reads 4 rows x 256 contiguous bytes (non-temporal), and
+// v_perm_b32 gathers element c of the 8 rows into the B fragment of tile c,
+// whose 16 columns are nl + c over the lanes: eight accumulator tiles
+// interleaved over the wave's 128 columns.  Tile c's D[i][j] sits in lane
+// (j, i / 4), component i % 4, so lane (l16, g) owns C[4 g + r][nl .. nl + 7]:
+// one 16-byte (16-bit C) or two (fp32 C) stores per activation row.
+// Workgroup, K split and partials as skinny_n_kernel, with 32-row chunks.
+// Requires N % 8 == 0 (lanes past N load the last 8 columns and store
+// nothing), ldb % 8 == 0, lda % 8 == 0 (or M == 1) and 16-byte aligned X, W.
+constexpr int SKH_WV = 8, SKH_KW = 4;
+constexpr int SKH_COLS = 128 * SKH_WV / SKH_KW;   // columns per workgroup
+
+template <typename T, typename TC, int WV, int KW, bool PARTIAL>
+__global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* part, int per) {
+    constexpr int CG = WV / KW;                  // column groups of 128 per workgroup
+    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * 8 * 64 : 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int cg = wave % CG, kw = wave / CG;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
+    const int nl = blockIdx.x * (128 * CG) + cg * 128 + 8 * l16;  // this lane's columns
+    const T* W = (const T*)p.W + min(nl, N - 8);
+    const T* X = (const T*)p.X + (int64_t)min(l16, M - 1) * p.lda;
+    const int64_t ldb = p.ldb;
+    const int chunks = (K + 31) / 32;
+    const int s_beg = (int)blockIdx.y * per;                      // the workgroup's slice
+    const int s_end = min(chunks, s_beg + per);
+    const int sub = (per + KW - 1) / KW;                          // this wave's part of it
+    const int c_beg = min(s_end, s_beg + kw * sub);
+    const int c_end = min(s_end, c_beg + sub);
+    const int f_end = max(c_beg, min(c_end, K / 32));             // chunks with 32 valid k
+
+    floatx4 acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int ch, u32x4 (&w)[8], u32x4& x) {
+        const int64_t k = (int64_t)ch * 32 + 8 * g;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = __builtin_nontemporal_load((const u32x4*)(W + (k + e) * ldb));
+        x = *(const u32x4*)(X + k);
+    };
+    // tile c: element c of the 8 rows, rows 2 d and 2 d + 1 in dword d
+    auto mma = [&](const u32x4 (&w)[8], const u32x4& x) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+            u32x4 b;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) b[d] = __builtin_amdgcn_perm(w[2 * d + 1][c >> 1], w[2 * d][c >> 1], sel);
+            acc[c] = mfma16<T>(x, b, acc[c]);
+        }
+    };
+    // full chunks, the next chunk's loads in flight
+    const int nf = f_end - c_beg;
+    int ch = c_beg;
+    {
+        u32x4 wa[8], xa, wb[8], xb;
+        int i = 0;
+        if (nf > 0) load(ch, wa, xa);
+        for (; i + 1 < nf; i += 2) {
+            load(ch + 1, wb, xb);
+            mma(wa, xa);
+            if (i + 2 < nf) load(ch + 2, wa, xa);
+            mma(wb, xb);
+            ch += 2;
+        }
+        if (i < nf) {
+            mma(wa, xa);
+            ++ch;
+        }
+    }
+    // the partial last chunk, k past K zero in both operands
+    for (; ch < c_end; ++ch) {
+        const int k = ch * 32 + 8 * g;
+        u32x4 w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            w[e] = k + e < K ? *(const u32x4*)(W + (int64_t)(k + e) * ldb) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 x = ld16_checked<T>(X + k, K - k);
+        mma(w, x);
+    }
+    // the KW parts of the slice, summed in wave order
+    if constexpr (KW > 1) {
+        if (kw > 0) {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) red[(((kw - 1) * CG + cg) * 8 + c) * 64 + lane] = acc[c];
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int j = 1; j < KW; ++j)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[c] += red[(((j - 1) * CG + cg) * 8 + c) * 64 + lane];
+    }
+
+    if (nl >= N) return;
+    if constexpr (PARTIAL) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m < M) {
+                float* dst = part + ((int64_t)blockIdx.y * M + m) * N + nl;
+                *(floatx4*)dst = floatx4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+                *(floatx4*)(dst + 4) = floatx4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+            }
+        }
+    } else {
+        float alpha = p.alpha, beta = p.beta;
+        if (p.mode == 1) {
+            alpha = *(const float*)p.alpha_dev;
+            beta = *(const float*)p.beta_dev;
+        } else if (p.mode == 2) {
+            alpha = (float)*(const _Float16*)p.alpha_dev;
+            beta = (float)*(const _Float16*)p.beta_dev;
+        }
+        float b8[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) b8[c] = p.epi.bias ? vkb::bias_at(p.epi, nl + c) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * g + r;
+            if (m >= M) continue;
+            TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
+            const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                float y = alpha * acc[c][r];
+                if (beta != 0.0f) y += beta * (float)src[c];
+                y += b8[c];
+                dst[c] = (TC)y;
+            }
+        }
+    }
+}
+
 template <typename T, typename TC, int MM, int RB>
 int launch_gemv(const SkParams& p, hipStream_t st) {
     const uint32_t grid = (p.N + RB - 1) / RB;
@@ -946,6 +1087,30 @@ int launch_skn(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) 
     return (int)hipGetLastError();
 }
 
+// skinny_nh_kernel K split: as skn_plan, over workgroups of SKH_COLS
+// columns and 32-row chunks (groups of 2 chunks, 64 k).
+inline SknPlan skh_plan(uint32_t N, uint32_t K) {
+    const uint32_t wg = (N + SKH_COLS - 1) / SKH_COLS;
+    const uint32_t groups = (K + 63) / 64;
+    uint32_t sp = 256 / wg;
+    if (sp > groups / 4) sp = groups / 4;
+    if (sp > 64) sp = 64;
+    if (sp < 1) sp = 1;
+    const uint32_t gper = (groups + sp - 1) / sp;
+    return SknPlan{(groups + gper - 1) / gper, 2 * gper};
+}
+
+template <typename T, typename TC>
+int launch_skh(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) {
+    const SknPlan pl = skh_plan(p.N, p.K);
+    const dim3 grid((p.N + SKH_COLS - 1) / SKH_COLS, nsplit), block(64 * SKH_WV);
+    if (nsplit > 1)
+        hipLaunchKernelGGL((skinny_nh_kernel<T, float, SKH_WV, SKH_KW, true>), grid, block, 0, st, p, part, (int)pl.per);
+    else
+        hipLaunchKernelGGL((skinny_nh_kernel<T, TC, SKH_WV, SKH_KW, false>), grid, block, 0, st, p, part, (int)pl.per);
+    return (int)hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint32_t N, uint32_t K, int64_t lda,
@@ -957,7 +1122,11 @@ extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint3
     if (ab_type == VKB_T_F32) {
         if (M > 16) return 0;
         if (!b_kmajor) return (N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(N, K).split;
-    } else if ((ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) || !b_kmajor || M > 64) {
+    } else if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) {
+        return 0;
+    } else if (!b_kmajor) {
+        return (M > 16 || N < 8 || N % 8 || ldb < (int64_t)N) ? 0 : skh_plan(N, K).split;
+    } else if (M > 64) {
         return 0;
     }
     // the staged kernels address a 32-row weight tile and the activation
@@ -1000,6 +1169,12 @@ extern "C" int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64
     if (ab_type == VKB_T_F32) {
         if (!b_kmajor) return launch_skn<float>(p, part, nsplit, st);
         return launch_sk_lds<float, float>(p, st);
+    }
+    if (!b_kmajor) {
+        if (ab_type == VKB_T_BF16)
+            return f32_out ? launch_skh<__bf16, float>(p, part, nsplit, st) : launch_skh<__bf16, __bf16>(p, part, nsplit, st);
+        return f32_out ? launch_skh<_Float16, float>(p, part, nsplit, st)
+                       : launch_skh<_Float16, _Float16>(p, part, nsplit, st);
     }
     return ab_type == VKB_T_BF16 ? launch_typed<__bf16>(p, f32_out, part, (int)nsplit, st)
                                  : launch_typed<_Float16>(p, f32_out, part, (int)nsplit, st);
