@@ -444,7 +444,7 @@ def main():
     log("[bench] decode 8192x8192, 24-64 tokens")
     line["fp16_decode_8192_wide"] = matvec(torch, vk, stream, args.steps, ntoks=(24, 32, 64))
     log("[bench] fp16 matvec 8192x8192, weight stored K x O")
-    line["fp16_matvec_8192_KxO"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8, 16), kxo=True)
+    line["fp16_matvec_8192_KxO"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8, 16, 32), kxo=True)
     log("[bench] fp32 matvec 8192x8192, both weight layouts")
     line["fp32_matvec_8192"] = matvec_f32(torch, vk, stream, args.steps)
     log("[bench] split-K and strided-batched")

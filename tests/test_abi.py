@@ -276,10 +276,11 @@ def test_plan_skinny_f32():
 
 
 def test_plan_skinny_16bit_kn():
-    """fp16 / bf16 with up to 16 activation rows and the weight stored K x N
+    """fp16 / bf16 with up to 64 activation rows and the weight stored K x N
     (op_b = N, PyTorch's x @ w): the 16-bit K x N kernel, N a multiple of 8,
     K split in 64-row groups so that the grid holds at most 256 workgroups of
-    256 columns, each slice at least 4 groups."""
+    256 columns (M <= 16) or 128 columns (17 <= M <= 64), each slice at least
+    4 groups."""
     for dt in (vk.DT_F16, vk.DT_BF16):
         for M in (1, 4, 16):
             pl = P(dt, dt, 0, 0, M, 8192, 8192, 8192, 8192, 8192)
@@ -288,8 +289,11 @@ def test_plan_skinny_16bit_kn():
         assert P(dt, dt, 0, 0, 1, 14336, 4096, 4096, 14336, 14336).split == 4
         assert P(dt, dt, 0, 0, 16, 4096, 14336, 14336, 4096, 4096).split == 16
         assert P(dt, dt, 0, 0, 4, 8, 32, 32, 8, 8).split == 1
-    # not this kernel: 17 rows, N % 8, ldb % 8, ldb short of N, lda % 8 (M > 1)
-    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    for M in (17, 32, 64):
+        assert P(vk.DT_F16, vk.DT_F16, 0, 0, M, 8192, 8192, 8192, 8192, 8192).split == 4   # 64 blocks x 4
+    assert P(vk.DT_BF16, vk.DT_BF16, 0, 0, 64, 1000, 1032, 1032, 1000, 1000).split == 4
+    # not this kernel: 65 rows, N % 8, ldb % 8, ldb short of N, lda % 8 (M > 1)
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8188, 8192, 8192, 8192, 8188).path != vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8192, 8192, 8192, 8196, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 4, 8192, 8192, 8192, 8184, 8192).path != vk.PATH_SKINNY

@@ -121,9 +121,9 @@ def _mark_skinny(vk, skinny=True):
     """an engine call whose path a case does not take (the decode kernels, or
     with skinny=False a 64x64 tile): a forwarded call leaves that path as
     vkblas_last_path"""
-    # 2 rows against W stored N x K: the decode kernels; 17 rows against W
+    # 2 rows against W stored N x K: the decode kernels; 65 rows against W
     # stored K x N (more than its decode kernel takes): a 64x64 tile
-    rows = 2 if skinny else 17
+    rows = 2 if skinny else 65
     x = torch.zeros(rows * 64, dtype=torch.float16, device="cuda:0")
     w = torch.zeros(64 * 64, dtype=torch.float16, device="cuda:0")
     y = torch.zeros(rows * 64, dtype=torch.float16, device="cuda:0")

@@ -184,7 +184,8 @@ def test_decode_deterministic():
 
 
 # Weight stored K x N (engine op_b = N, PyTorch's x @ w): the 16-bit K x N
-# kernel for up to 16 activation rows, N a multiple of 8.  (M, N, K, pad_a,
+# kernel for up to 64 activation rows (one to four 16-row tiles), N a
+# multiple of 8.  (M, N, K, pad_a,
 # pad_b, beta, out): ldb = N + pad_b with NaN in the padding columns; ragged K
 # (not a multiple of the 32-row chunk), N not a multiple of the workgroup's
 # 256 columns, K split over the grid with fp32 partials and the reduce.
@@ -200,6 +201,14 @@ CASES_KN += [
     (4, 776, 7, 1, 0, 0.25, "f16"),           # a partial chunk only
     (12, 1032, 2056, 8, 24, 1.0, "bf16"),
     (2, 8, 4104, 0, 8, 0.0, "f32"),
+    # 17-64 rows: two to four activation tiles, 128-column workgroups
+    (17, 8192, 8192, 0, 0, 0.0, "f16"),
+    (24, 1000, 1032, 8, 8, 0.5, "bf16"),
+    (33, 264, 4100, 4, 0, 0.0, "f16>f32"),
+    (48, 4096, 520, 8, 16, -0.5, "f16"),
+    (64, 8192, 2056, 0, 8, 0.25, "bf16>f32"),
+    (64, 136, 33, 7, 0, 0.0, "f16"),
+    (57, 2048, 65536, 0, 0, 0.0, "bf16"),
 ]
 
 
@@ -241,7 +250,7 @@ def test_decode_kn(case):
     assert normwise(g, w) <= (BF16_BOUND if bf and not f32 else F16_BOUND)
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1000, 1032), (7, 8192, 8192)])
+@pytest.mark.parametrize("M,N,K", [(1, 1000, 1032), (7, 8192, 8192), (40, 520, 1032), (64, 4096, 4096)])
 @pytest.mark.parametrize("sep", [False, True])
 def test_decode_kn_epilogue(M, N, K, sep):
     """bias and a separate C input on the K x N kernel: in its own epilogue,
@@ -273,7 +282,7 @@ def test_decode_kn_deterministic():
     import vkblas_amd as vk
     from gpu_helpers import to_dev, to_host
     print("[case] decode K x N determinism", flush=True)
-    for M, N, K in ((1, 8192, 8192), (16, 4096, 14336), (5, 1000, 1032)):
+    for M, N, K in ((1, 8192, 8192), (16, 4096, 14336), (5, 1000, 1032), (40, 8192, 8192), (64, 1000, 1032)):
         dX, dW = to_dev(_padded(M, K, K, 41, 1.0)), to_dev(_padded(K, N, N, 42, 0.05))
         outs = []
         for _ in range(3):

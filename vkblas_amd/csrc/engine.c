@@ -345,9 +345,8 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (split_k == 0 && g_force_split) split_k = g_force_split;
 
     /* decode-shaped: X[M, K] (K-contiguous rows) against a weight W.
-     * fp16 / bf16: M <= 64 with W stored N x K (op_b = T), M <= 16 with W
-     * stored K x N (op_b = N); fp32: M <= 16, W stored N x K or K x N, fp32
-     * output.  vkb_skinny_plan holds the
+     * fp16 / bf16: M <= 64, W stored N x K (op_b = T) or K x N (op_b = N);
+     * fp32: M <= 16, W stored N x K or K x N, fp32 output.  vkb_skinny_plan holds the
      * kernels' own limits (leading dimensions, 32-bit buffer spans) and
      * returns their K split, or 0: then a tile path. */
     if (op_a == VKBLAS_OP_N && batch == 1 && split_k <= 1 && aligned && !g_no_skinny &&

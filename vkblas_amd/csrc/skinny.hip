@@ -816,23 +816,30 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
 // interleaved over the wave's 128 columns.  Tile c's D[i][j] sits in lane
 // (j, i / 4), component i % 4, so lane (l16, g) owns C[4 g + r][nl .. nl + 7]:
 // one 16-byte (16-bit C) or two (fp32 C) stores per activation row.
+// MT activation tiles of 16 rows (M up to 16 MT) share each B fragment.
 // Workgroup, K split and partials as skinny_n_kernel, with 32-row chunks.
 // Requires N % 8 == 0 (lanes past N load the last 8 columns and store
 // nothing), ldb % 8 == 0, lda % 8 == 0 (or M == 1) and 16-byte aligned X, W.
+// Geometries: M <= 16 eight waves (two column groups, four along K); 17 <= M
+// <= 64 four waves (one column group of 128, four along K), whose 4 MT x 8
+// accumulator tiles need the register file of one wave per SIMD.
 constexpr int SKH_WV = 8, SKH_KW = 4;
-constexpr int SKH_COLS = 128 * SKH_WV / SKH_KW;   // columns per workgroup
+constexpr int SKH_COLS = 128 * SKH_WV / SKH_KW;   // columns per workgroup, M <= 16
+constexpr int SKH_COLS_MT = 128;                  // columns per workgroup, M > 16
 
-template <typename T, typename TC, int WV, int KW, bool PARTIAL>
+template <typename T, typename TC, int WV, int KW, int MT, bool PARTIAL>
 __global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* part, int per) {
     constexpr int CG = WV / KW;                  // column groups of 128 per workgroup
-    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * 8 * 64 : 1];
+    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * MT * 8 * 64 : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cg = wave % CG, kw = wave / CG;
     const int l16 = lane & 15, g = lane >> 4;
     const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
     const int nl = blockIdx.x * (128 * CG) + cg * 128 + 8 * l16;  // this lane's columns
     const T* W = (const T*)p.W + min(nl, N - 8);
-    const T* X = (const T*)p.X + (int64_t)min(l16, M - 1) * p.lda;
+    const T* X[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) X[t] = (const T*)p.X + (int64_t)min(16 * t + l16, M - 1) * p.lda;
     const int64_t ldb = p.ldb;
     const int chunks = (K + 31) / 32;
     const int s_beg = (int)blockIdx.y * per;                      // the workgroup's slice
@@ -842,31 +849,35 @@ __global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* p
     const int c_end = min(s_end, c_beg + sub);
     const int f_end = max(c_beg, min(c_end, K / 32));             // chunks with 32 valid k
 
-    floatx4 acc[8];
+    floatx4 acc[MT][8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto load = [&](int ch, u32x4 (&w)[8], u32x4& x) {
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[t][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int ch, u32x4 (&w)[8], u32x4 (&x)[MT]) {
         const int64_t k = (int64_t)ch * 32 + 8 * g;
 #pragma unroll
         for (int e = 0; e < 8; ++e) w[e] = __builtin_nontemporal_load((const u32x4*)(W + (k + e) * ldb));
-        x = *(const u32x4*)(X + k);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) x[t] = *(const u32x4*)(X[t] + k);
     };
     // tile c: element c of the 8 rows, rows 2 d and 2 d + 1 in dword d
-    auto mma = [&](const u32x4 (&w)[8], const u32x4& x) {
+    auto mma = [&](const u32x4 (&w)[8], const u32x4 (&x)[MT]) {
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
             const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
             u32x4 b;
 #pragma unroll
             for (int d = 0; d < 4; ++d) b[d] = __builtin_amdgcn_perm(w[2 * d + 1][c >> 1], w[2 * d][c >> 1], sel);
-            acc[c] = mfma16<T>(x, b, acc[c]);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) acc[t][c] = mfma16<T>(x[t], b, acc[t][c]);
         }
     };
     // full chunks, the next chunk's loads in flight
     const int nf = f_end - c_beg;
     int ch = c_beg;
     {
-        u32x4 wa[8], xa, wb[8], xb;
+        u32x4 wa[8], xa[MT], wb[8], xb[MT];
         int i = 0;
         if (nf > 0) load(ch, wa, xa);
         for (; i + 1 < nf; i += 2) {
@@ -888,34 +899,42 @@ __global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* p
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             w[e] = k + e < K ? *(const u32x4*)(W + (int64_t)(k + e) * ldb) : u32x4{0u, 0u, 0u, 0u};
-        const u32x4 x = ld16_checked<T>(X + k, K - k);
+        u32x4 x[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) x[t] = ld16_checked<T>(X[t] + k, K - k);
         mma(w, x);
     }
     // the KW parts of the slice, summed in wave order
     if constexpr (KW > 1) {
         if (kw > 0) {
 #pragma unroll
-            for (int c = 0; c < 8; ++c) red[(((kw - 1) * CG + cg) * 8 + c) * 64 + lane] = acc[c];
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) red[((((kw - 1) * CG + cg) * MT + t) * 8 + c) * 64 + lane] = acc[t][c];
         }
         __syncthreads();
         if (kw > 0) return;
 #pragma unroll
         for (int j = 1; j < KW; ++j)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) acc[c] += red[(((j - 1) * CG + cg) * 8 + c) * 64 + lane];
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[t][c] += red[((((j - 1) * CG + cg) * MT + t) * 8 + c) * 64 + lane];
     }
 
     if (nl >= N) return;
     if constexpr (PARTIAL) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            if (m < M) {
-                float* dst = part + ((int64_t)blockIdx.y * M + m) * N + nl;
-                *(floatx4*)dst = floatx4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-                *(floatx4*)(dst + 4) = floatx4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * t + 4 * g + r;
+                if (m < M) {
+                    float* dst = part + ((int64_t)blockIdx.y * M + m) * N + nl;
+                    *(floatx4*)dst = floatx4{acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]};
+                    *(floatx4*)(dst + 4) = floatx4{acc[t][4][r], acc[t][5][r], acc[t][6][r], acc[t][7][r]};
+                }
             }
-        }
     } else {
         float alpha = p.alpha, beta = p.beta;
         if (p.mode == 1) {
@@ -929,19 +948,21 @@ __global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* p
 #pragma unroll
         for (int c = 0; c < 8; ++c) b8[c] = p.epi.bias ? vkb::bias_at(p.epi, nl + c) : 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            if (m >= M) continue;
-            TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
-            const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+        for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                float y = alpha * acc[c][r];
-                if (beta != 0.0f) y += beta * (float)src[c];
-                y += b8[c];
-                dst[c] = (TC)y;
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * t + 4 * g + r;
+                if (m >= M) continue;
+                TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
+                const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    float y = alpha * acc[t][c][r];
+                    if (beta != 0.0f) y += beta * (float)src[c];
+                    y += b8[c];
+                    dst[c] = (TC)y;
+                }
             }
-        }
     }
 }
 
@@ -1088,9 +1109,11 @@ int launch_skn(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) 
 }
 
 // skinny_nh_kernel K split: as skn_plan, over workgroups of SKH_COLS
-// columns and 32-row chunks (groups of 2 chunks, 64 k).
-inline SknPlan skh_plan(uint32_t N, uint32_t K) {
-    const uint32_t wg = (N + SKH_COLS - 1) / SKH_COLS;
+// (M <= 16) or SKH_COLS_MT columns and 32-row chunks (groups of 2 chunks,
+// 64 k).
+inline SknPlan skh_plan(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t cols = M <= 16 ? SKH_COLS : SKH_COLS_MT;
+    const uint32_t wg = (N + cols - 1) / cols;
     const uint32_t groups = (K + 63) / 64;
     uint32_t sp = 256 / wg;
     if (sp > groups / 4) sp = groups / 4;
@@ -1100,14 +1123,25 @@ inline SknPlan skh_plan(uint32_t N, uint32_t K) {
     return SknPlan{(groups + gper - 1) / gper, 2 * gper};
 }
 
+template <typename T, typename TC, int WV, int MT>
+void launch_skh_mt(const SkParams& p, float* part, uint32_t nsplit, int per, hipStream_t st) {
+    constexpr int cols = 128 * WV / SKH_KW;
+    const dim3 grid((p.N + cols - 1) / cols, nsplit), block(64 * WV);
+    if (nsplit > 1)
+        hipLaunchKernelGGL((skinny_nh_kernel<T, float, WV, SKH_KW, MT, true>), grid, block, 0, st, p, part, per);
+    else
+        hipLaunchKernelGGL((skinny_nh_kernel<T, TC, WV, SKH_KW, MT, false>), grid, block, 0, st, p, part, per);
+}
+
 template <typename T, typename TC>
 int launch_skh(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) {
-    const SknPlan pl = skh_plan(p.N, p.K);
-    const dim3 grid((p.N + SKH_COLS - 1) / SKH_COLS, nsplit), block(64 * SKH_WV);
-    if (nsplit > 1)
-        hipLaunchKernelGGL((skinny_nh_kernel<T, float, SKH_WV, SKH_KW, true>), grid, block, 0, st, p, part, (int)pl.per);
-    else
-        hipLaunchKernelGGL((skinny_nh_kernel<T, TC, SKH_WV, SKH_KW, false>), grid, block, 0, st, p, part, (int)pl.per);
+    const int per = (int)skh_plan(p.M, p.N, p.K).per;
+    switch ((p.M + 15) / 16) {
+        case 1: launch_skh_mt<T, TC, SKH_WV, 1>(p, part, nsplit, per, st); break;
+        case 2: launch_skh_mt<T, TC, 4, 2>(p, part, nsplit, per, st); break;
+        case 3: launch_skh_mt<T, TC, 4, 3>(p, part, nsplit, per, st); break;
+        default: launch_skh_mt<T, TC, 4, 4>(p, part, nsplit, per, st); break;
+    }
     return (int)hipGetLastError();
 }
 
@@ -1125,7 +1159,7 @@ extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint3
     } else if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) {
         return 0;
     } else if (!b_kmajor) {
-        return (M > 16 || N < 8 || N % 8 || ldb < (int64_t)N) ? 0 : skh_plan(N, K).split;
+        return (M > 64 || N < 8 || N % 8 || ldb < (int64_t)N) ? 0 : skh_plan(M, N, K).split;
     } else if (M > 64) {
         return 0;
     }
