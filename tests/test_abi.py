@@ -302,6 +302,25 @@ def test_plan_skinny_16bit_kn():
     assert P(vk.DT_BF16, vk.DT_BF16, 0, 0, 1, 8192, 8192, 3, 8192, 8192).path == vk.PATH_SKINNY
 
 
+def test_plan_split_mid_size_m():
+    """Mid-size M against a large weight (prefill-like shapes): at most 128
+    output tiles of 128x128 and K >= 4096 split K so the grid fills the CUs.
+    Pipelined 128x128 tiles (M >= 128) take 256 / tiles slices; M below 128
+    (the generic 128x128 kernel) takes min(K / 1024, 512 / tiles, 128)."""
+    for dt in (vk.DT_F16, vk.DT_BF16, vk.DT_F32):
+        for ob in (0, 1):
+            def pl(M, N=8192, K=8192):
+                return P(dt, dt, 0, ob, M, N, K, K, K if ob else N, N)
+            assert (pl(128).path, pl(128).split, pl(128).tile) == (vk.PATH_SPLITK, 4, 1)     # 64 tiles
+            assert (pl(256).path, pl(256).split) == (vk.PATH_SPLITK, 2)                      # 128 tiles
+            assert (pl(192).path, pl(192).split) == (vk.PATH_SPLITK, 2)                      # 128 tiles, edge row
+            assert (pl(65).path, pl(65).split, pl(65).tile) == (vk.PATH_SPLITK, 8, 1)        # generic, 64 tiles
+            assert pl(384).split == 1 and pl(384).path != vk.PATH_SPLITK                     # 192 tiles
+            assert pl(128, K=2048).split == 1                                                # K below 4096
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 1024, 1024, 8192, 8192, 1024, 1024).split == 4
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, 2048, 1024, 8192, 8192, 1024, 1024).split == 2
+
+
 def test_plan_decode_span_limit():
     """The decode kernels address a 32-row weight tile and the activation
     rows with 32-bit buffer offsets; a decode-shaped call whose leading

@@ -394,12 +394,16 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 (uint64_t)cdiv(M, 128) * cdiv(N, 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
                 tile = VKB_TILE_128;
         } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
-                   (uint64_t)cdiv(M, 128) * cdiv(N, 128) < 64 && K >= 4096) {
-            /* Whole 128x128 tiles, fewer than 64 of them, and a long K: the
-             * pipelined kernel runs pass 1 on 128x128 tiles with 256 / tiles
-             * slices, a workgroup per CU.  Each workgroup reads its A and B
-             * slices once; the tiles of one slice sit on one XCD and share
-             * those reads in L2.
+                   (uint64_t)cdiv(M, 128) * cdiv(N, 128) <= 128 && K >= 4096) {
+            /* 128x128 tiles, at most 128 of them (at most half the CUs), and
+             * a long K: the pipelined kernel runs pass 1 on 128x128 tiles
+             * with 256 / tiles slices, a workgroup per CU.  Each workgroup
+             * reads its A and B slices once; the tiles of one slice sit on
+             * one XCD and share those reads in L2.
+             * Mid-size M against a large weight (fp16, N = K = 8192, one
+             * box): M = 128 (64 tiles) 73.0 -> 43.0 us with 4 slices, M = 192
+             * / 256 (128 tiles) 71.7 / 70.9 -> 54.8 / 56.8 us with 2; 192
+             * tiles (M = 384) are fastest unsplit.
              * 16-bit inputs (HBM-bound here): the launcher runs four LDS
              * stages (three K steps of loads in flight).  Measured at
              * M = N = 256, fp16, K = 262144: 54.5 us (4.9 TB/s) against
@@ -425,10 +429,12 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
              * of each A / B slice over 128 columns / rows) when the output
              * allows; slices of at least 1024 k; up to ~512 workgroups (two
              * per CU) and 128 slices.  Measured at M = N = 256: K = 65536 ->
-             * 64 slices, K = 262144 -> 128 slices are the fastest choices. */
+             * 64 slices, K = 262144 -> 128 slices are the fastest choices;
+             * M = 65 / 96 against N = K = 8192 (64 generic 128x128 tiles):
+             * 147.1 / 143.7 -> 43.5 / 49.5 us with 8 slices. */
             const int stile = (M >= 128 && N >= 128 && g_force_tile < 0) ? VKB_TILE_128 : tile;
             uint64_t tiles = (uint64_t)cdiv(M, vkb_tile_bm(stile)) * cdiv(N, vkb_tile_bn(stile));
-            if (tiles < 64 && K >= 4096) {
+            if (tiles <= 128 && K >= 4096) {
                 uint64_t want = K / 1024;
                 if (want > 512 / tiles) want = 512 / tiles;
                 if (want > 128) want = 128;
