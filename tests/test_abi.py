@@ -217,6 +217,14 @@ def test_plan_tile_crossover():
     for dt in (vk.DT_F16, vk.DT_BF16):
         assert [tile(dt, n) for n in (2048, 2560, 2816, 3072, 3584, 4096, 6144)] == [T128, T128, T128, T256, T256,
                                                                                       T256, T256]
+    # exactly 128 tiles of 256x256 (half the CUs): 128x128 tiles; 144: 256x256
+    for dt in (vk.DT_F16, vk.DT_BF16):
+        for (m, n, k) in ((2048, 4096, 4096), (1024, 8192, 8192), (4096, 2048, 8192)):
+            assert P(dt, dt, 0, 1, m, n, k, k, k, n, split_k=1).path == T128
+        assert P(dt, dt, 0, 1, 4096, 2304, 4096, 4096, 4096, 2304, split_k=1).path == T256
+        # and with a very long K, 2 slices of 256x256 tiles
+        pl = P(dt, dt, 0, 1, 1024, 8192, 28672, 28672, 28672, 8192)
+        assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 2, 2)
     # a shape only the generic kernels take keeps the size rule (fp32 5000^3: 256x256 tiles)
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 5000, 5000, 5000, 5000, 5000, 5000).path == T256
 

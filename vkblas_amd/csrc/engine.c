@@ -371,15 +371,17 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
          *   (5120^3 131.5 against 116.3 TFLOP/s, 6144^3 147.7 / 110.9;
          *   4096^3 and the 64 x 512^3 batch equal): 256x256 only for about
          *   whole waves.
-         * - 16-bit: 256x256 tiles from 128 of them on (3072^3 fp16 963 against
-         *   793 TFLOP/s, 3584^3 1154-1245 / 1017-1048; 2560^3, 100 tiles:
-         *   656 against 989). */
+         * - 16-bit: 256x256 tiles from more than 128 of them on (3072^3
+         *   fp16, 144 tiles, 963 against 793 TFLOP/s, 3584^3 1154-1245 /
+         *   1017-1048; 2560^3, 100 tiles: 656 against 989; exactly 128,
+         *   half the CUs: 2048 x 4096 x 4096 81.1 against 58.8 us, 1024 x
+         *   8192 x 8192 144.0 against 112.3). */
         const uint64_t t256 = (uint64_t)cdiv(M, 256) * cdiv(N, 256) * batch;
         if (ab_type == VKBLAS_DT_F32 && tile == VKB_TILE_256 &&
             pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
             8 * t256 < 7 * 256 * ((t256 + 255) / 256))
             tile = VKB_TILE_128;
-        if (ab_type != VKBLAS_DT_F32 && tile == VKB_TILE_128 && t256 >= 128 &&
+        if (ab_type != VKBLAS_DT_F32 && tile == VKB_TILE_128 && t256 > 128 &&
             pipe_ok(ab_type, VKB_TILE_256, op_a, op_b, M, N, K, lda, ldb, aligned))
             tile = VKB_TILE_256;
     }
@@ -424,6 +426,16 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 split = cdiv(K, kps);
                 tile = VKB_TILE_128;
             }
+        } else if (split_k == 0 && g_force_tile < 0 && ab_type != VKBLAS_DT_F32 && K >= 16384 &&
+                   pipe_ok(ab_type, VKB_TILE_256, op_a, op_b, M, N, K, lda, ldb, aligned) &&
+                   (uint64_t)cdiv(M, 256) * cdiv(N, 256) > 64 && (uint64_t)cdiv(M, 256) * cdiv(N, 256) <= 128) {
+            /* 16-bit, 65-128 tiles of 256x256 (a quarter to a half of the
+             * CUs) and a very long K: 256 / tiles slices of 256x256 tiles
+             * rather than unsplit 128x128 ones.  1024 x 8192 x 28672 fp16
+             * (128 tiles, one box): 393.4 against 524.4 us; at K = 14336
+             * the two are level (195.3 / 198.9), at 8192 128x128 wins. */
+            split = 256 / (uint32_t)((uint64_t)cdiv(M, 256) * cdiv(N, 256));
+            tile = VKB_TILE_256;
         } else if (split_k == 0) {
             /* Few output tiles and a long K: split K.  128x128 tiles (reuse
              * of each A / B slice over 128 columns / rows) when the output
