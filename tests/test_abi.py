@@ -313,8 +313,9 @@ def test_plan_skinny_16bit_kn():
 def test_plan_split_mid_size_m():
     """Mid-size M against a large weight (prefill-like shapes): at most 128
     output tiles of 128x128 and K >= 4096 split K so the grid fills the CUs.
-    Pipelined 128x128 tiles (M >= 128) take 256 / tiles slices; M below 128
-    (the generic 128x128 kernel) takes min(K / 1024, 512 / tiles, 128)."""
+    Pipelined 128x128 tiles (M >= 65 with K-major A; A rows past M read as
+    row M - 1) take 256 / tiles slices; the generic kernel's tiles take
+    min(K / 1024, 512 / tiles, 128)."""
     for dt in (vk.DT_F16, vk.DT_BF16, vk.DT_F32):
         for ob in (0, 1):
             def pl(M, N=8192, K=8192):
@@ -322,9 +323,14 @@ def test_plan_split_mid_size_m():
             assert (pl(128).path, pl(128).split, pl(128).tile) == (vk.PATH_SPLITK, 4, 1)     # 64 tiles
             assert (pl(256).path, pl(256).split) == (vk.PATH_SPLITK, 2)                      # 128 tiles
             assert (pl(192).path, pl(192).split) == (vk.PATH_SPLITK, 2)                      # 128 tiles, edge row
-            assert (pl(65).path, pl(65).split, pl(65).tile) == (vk.PATH_SPLITK, 8, 1)        # generic, 64 tiles
+            assert (pl(65).path, pl(65).split, pl(65).tile) == (vk.PATH_SPLITK, 4, 1)        # short M, 64 tiles
             assert pl(384).split == 1 and pl(384).path != vk.PATH_SPLITK                     # 192 tiles
             assert pl(128, K=2048).split == 1                                                # K below 4096
+    # fp32 from 17 to 64 rows and short M with MN-major A: the generic kernel
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 1, 64, 4096, 4096, 4096, 4096, 4096)
+    assert pl.path in (vk.PATH_SPLITK, vk.PATH_TILE64) and pl.tile == 0
+    pl = P(vk.DT_F16, vk.DT_F16, 1, 1, 96, 8192, 8192, 96, 8192, 8192)
+    assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 8, 1)
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 1024, 1024, 8192, 8192, 1024, 1024).split == 4
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 2048, 1024, 8192, 8192, 1024, 1024).split == 2
 
@@ -378,8 +384,11 @@ def test_plan_split_heuristic_and_off():
     # slices of whole K-step pairs
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 64 == 0 and 4 * pl.split <= 256
-    # below the tile in M: the generic 64x64 split
+    # below the tile in M: from 65 rows (K-major A) the pipelined 128x128
+    # pass 1 (rows past M read as row M - 1), up to 64 rows the generic 64x64
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 100, 256, 65536, 65536, 256, 256)
+    assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 64 == 0
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 60, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 0
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=1)
     assert pl.path != vk.PATH_SPLITK

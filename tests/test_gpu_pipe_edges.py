@@ -28,7 +28,9 @@ pytestmark = pytest.mark.gpu
 TYPES = [("f32", "f32"), ("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32")]
 # tile override, tile edge, M, N (n8 form), K
 TILES = {"pipe256": (2, 256, 552, 536, 256), "pipe128x2": (1, 128, 2344, 2328, 128),
-         "pipe128x4": (1, 128, 296, 280, 256)}
+         "pipe128x4": (1, 128, 296, 280, 256),
+         # M below the 128-row tile: K-major A reads rows past M as row M - 1
+         "pipe128short": (1, 128, 100, 280, 256), "pipe128m66": (1, 128, 66, 536, 256)}
 GUARD_ROWS = 3
 
 
@@ -65,11 +67,13 @@ def _host(t: torch.Tensor) -> np.ndarray:
 
 
 def expected_kernel(ab, edge, M, N, op_a, op_b):
-    """the launcher's rule: edge tiles need M >= BM, N >= BN, N % 4 == 0 and
-    an MN-major operand's ragged dimension a multiple of 16 bytes"""
+    """the launcher's rule: edge tiles need M >= BM (or 128x128 tiles with
+    K-major A), N >= BN, N % 4 == 0 and an MN-major operand's ragged dimension
+    a multiple of 16 bytes"""
     vec = 4 if ab == "f32" else 8
     ak, bk = op_a == 0, op_b == 1
-    if not (M >= edge and N >= edge and N % 4 == 0 and (ak or M % vec == 0) and (bk or N % vec == 0)):
+    m_ok = M >= edge or (edge == 128 and ak)
+    if not (m_ok and N >= edge and N % 4 == 0 and (ak or M % vec == 0) and (bk or N % vec == 0)):
         return 2                                  # generic kernel, checked edges
     if edge == 256:
         return 3

@@ -130,7 +130,8 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
         constexpr uint32_t KPAIR = 256 / sizeof(T);
         const uint64_t span_a = ((uint64_t)(a->a_kmajor ? bm : a->K) * (uint64_t)a->lda + a->K) * ES;
         const uint64_t span_b = ((uint64_t)(a->b_kmajor ? bn : a->K) * (uint64_t)a->ldb + a->K) * ES;
-        const bool edges_ok = a->M >= (uint32_t)bm && a->N >= (uint32_t)bn && a->N % 4 == 0 &&
+        // M < bm: 128x128 tiles with K-major A (rows past M read as row M - 1)
+        const bool edges_ok = (a->M >= (uint32_t)bm || (bm == 128 && ak)) && a->N >= (uint32_t)bn && a->N % 4 == 0 &&
                               (a->a_kmajor || a->M % VEC == 0) && (a->b_kmajor || a->N % VEC == 0);
         const bool tiles_ok = !p.ptr_array && (a->K % BK == 0) && p.vec_a && p.vec_b && p.vec_c &&
                               (full || edges_ok);

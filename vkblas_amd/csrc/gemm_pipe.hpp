@@ -159,9 +159,12 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // only those from its own start m_lo on, which the tile before it does
     // not store (likewise for columns).  Nothing is stored twice, so beta
     // != 0 reads each C element once.
+    // Short M (128x128 tiles with K-major A only, M < BM): the one tile row
+    // starts at row 0, A rows past M - 1 are read as row M - 1 and C rows
+    // from M on are not stored.
     const int m_lo = (int)(first_m + tin % gm) * BM;
     const int n_lo = (int)(tin / gm) * BN;
-    const int m0 = min(m_lo, (int)p.M - BM);
+    const int m0 = max(0, min(m_lo, (int)p.M - BM));
     const int n0 = min(n_lo, (int)p.N - BN);
 
     const int lda = (int)p.lda, ldb = (int)p.ldb;
@@ -188,6 +191,13 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // every instruction; the row step 8 i and k0 go in soffset.
     const int koff = ((lane & 7) ^ (lane >> 3)) << 4;
     const int a_voff = ((BM / 4) * wave + (lane >> 3)) * lda * ES + koff;
+    // 128x128 tiles: one VGPR offset per instruction, its row clamped to the
+    // last row of A (a no-op unless M < BM)
+    constexpr int NAV = (WT == 64 && AK) ? NDMA : 1;
+    int a_vn[NAV];
+#pragma unroll
+    for (int n = 0; n < NAV; ++n)
+        a_vn[n] = min((BM / 4) * wave + (lane >> 3) + 8 * n, (int)p.M - 1 - m0) * lda * ES + koff;
     const int b_voff = ((BN / 4) * wave + (lane >> 3)) * ldb * ES + koff;
     // 16-bit MN-major direct loads: instruction n of this wave fills the
     // 1-KiB block NDMA wave + n (k rows RPB (NDMA wave + n) + [0, RPB); lane ->
@@ -260,7 +270,9 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     auto dma_load = [&](int kt, int S, int n) {
         const int k0 = kt * BK;
         if (n < NDMA) {
-            if constexpr (AK)
+            if constexpr (AK && NAV > 1)
+                dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * GRP], a_vn[n], k0 * ES);
+            else if constexpr (AK)
                 dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * GRP], a_voff, (k0 + n * 8 * lda) * ES);
             else if constexpr (ATR)
                 dma(true, (lds_ptr_t)&lds[A0 + S * STG + (NDMA * wave + n) * 64], a_tr[trv(n)],
@@ -617,7 +629,8 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
                 const u32x4 v = *(const u32x4*)(wl + r * STR + c * 16);
                 // an edge tile's chunks start on n_lo: the launcher takes this
                 // path only where N is a multiple of 16 bytes of C
-                const bool mine = m0 + wm * WT + pass * PROWS + r >= m_lo &&
+                const int row = m0 + wm * WT + pass * PROWS + r;
+                const bool mine = row >= m_lo && row < (int)p.M &&
                                   n0 + wn * WT + c * (16 / (int)sizeof(TC)) >= n_lo;
                 if (mine)
                     __builtin_nontemporal_store(v, (u32x4*)((char*)(cblk + (int64_t)(pass * PROWS + r) * p.ldc) + c * 16));
@@ -635,7 +648,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
 #pragma unroll
         for (int i = 0; i < NF; ++i) {
             const int m = m0 + wm * WT + i * FR + fl;
-            if (m < m_lo) continue;   // stored by the tile before an edge tile
+            if (m < m_lo || m >= (int)p.M) continue;   // stored by the tile before an edge tile; past M
             TC* crow = Cb + (int64_t)m * p.ldc;
             const TC* cirow = Ci + (int64_t)m * p.epi.ldcin;
 #pragma unroll
