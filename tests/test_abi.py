@@ -163,11 +163,11 @@ def test_plan_headline_configs():
     for n in (2048, 4096, 8192):
         assert P(vk.DT_F16, vk.DT_F16, 0, 0, n, n, n, n, n, n).path in (vk.PATH_TILE128, vk.PATH_TILE256)
     # config 4: decode (engine op_a = N, op_b = T, M = tokens)
-    for ntok in (1, 4, 8, 16, 17, 32, 40):
+    for ntok in (1, 4, 8, 16, 17, 24):
         for dt in (vk.DT_F16, vk.DT_BF16):
             pl = P(dt, dt, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192)
             assert pl.path == vk.PATH_SKINNY
-    # 41-64 tokens at 8192^2: the short-M pipelined tiles with a K split
+    # 25-64 tokens at 8192^2: the short-M pipelined tiles with a K split
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 64, 8192, 8192, 8192, 8192, 8192).path == vk.PATH_SPLITK
     # 65 tokens: a GEMM again
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
@@ -242,17 +242,18 @@ def test_plan_decode_split():
         return pl.split
     for M in (1, 2, 3, 16):
         assert split(M, 8192, 8192) == 1
-    for M in (17, 24, 40):
+    for M in (17, 24):
         assert split(M, 8192, 8192) == 4      # 64 workgroups per slice
         assert split(M, 14336, 4096) == 2     # 112 per slice: 224 workgroups
         assert split(M, 4096, 14336) == 8     # 32 per slice
-    # 41-64 rows: the decode kernels where the short-M tiles do not apply
-    # (K below 4096, more than 128 column tiles)
+    assert split(32, 4096, 14336) == 8
+    # 25-64 rows (33-64 against N < 8192): the decode kernels where the
+    # short-M tiles do not apply (K below 4096, more than 128 column tiles)
     assert split(64, 8192, 2048) == 4 and split(48, 40000, 8192) == 1
     # and otherwise the short-M pipelined tiles with a K split
-    for M in (41, 64):
-        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, M, 8192, 8192, 8192, 8192, 8192)
-        assert (pl.path, pl.tile, pl.split) == (vk.PATH_SPLITK, 1, 4)
+    for M, N in ((25, 8192), (64, 8192), (33, 4096)):
+        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, M, N, 8192, 8192, 8192, N)
+        assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 1) and pl.split >= 2
     assert split(32, 256, 8192) == 16         # 2 per slice, 64 steps: 4 per slice
     assert split(32, 256, 1024) == 2          # 8 steps: at least 4 per slice
     assert split(32, 40000, 8192) == 1        # more than one round already

@@ -158,11 +158,11 @@ def test_split_k(ab, ct, split, beta, sep):
 @pytest.mark.parametrize("beta,sep", [(0.0, False), (0.5, True)])
 def test_decode(dt, tokens, beta, sep):
     """decode shapes (engine op_a = N, op_b = T): GEMV, staged skinny, staged
-    decode (24 and 40 tokens at K = 4096 split K); 64 tokens: the short-M
+    decode (24 tokens at K = 4096 splits K); 40 and 64 tokens: the short-M
     pipelined 128x128 tiles with a K split and the reduce's epilogue"""
     import vkblas_amd as vk
     run_case(dt, dt, 0, 1, tokens, 4096, 4096, 1.0, beta, dt, sep,
-             expect_path=vk.PATH_SKINNY if tokens <= 40 else vk.PATH_SPLITK, scale_b=0.05)
+             expect_path=vk.PATH_SKINNY if tokens <= 32 else vk.PATH_SPLITK, scale_b=0.05)
 
 
 @pytest.mark.parametrize("ab,ct", [("f32", "f32"), ("f16", "f16"), ("bf16", "bf16")])

@@ -311,10 +311,10 @@ static int pipe_ok(vkblas_dtype_t ab_type, int tile, vkblas_op_t op_a, vkblas_op
      * 65 rows (fewer waste three quarters of the tile's MFMAs or more: fp32
      * M = 64 / 32 against N = K = 8192 took 124 / 122 us there, 84 / 130 on
      * the generic kernel; M = 65 / 96 fp32 207 / 206 -> 131 / 132 us, fp16
-     * 42.2 / 49.7 -> 36.9 / 38.5), 16-bit from 41 (the planner prefers them
+     * 42.2 / 49.7 -> 36.9 / 38.5), 16-bit from 25 (the planner prefers them
      * to the decode kernels there, see below) */
     return aligned && !g_generic_only &&
-           (M >= edge || (tile == VKB_TILE_128 && op_a == VKBLAS_OP_N && M > (ab_type == VKBLAS_DT_F32 ? 64u : 40u))) &&
+           (M >= edge || (tile == VKB_TILE_128 && op_a == VKBLAS_OP_N && M > (ab_type == VKBLAS_DT_F32 ? 64u : 24u))) &&
            N >= edge && N % 4 == 0 &&
            (op_a == VKBLAS_OP_N || M % vec == 0) && (op_b == VKBLAS_OP_T || N % vec == 0) && K % kpair == 0 &&
            lda % vec == 0 && ldb % vec == 0;
@@ -357,14 +357,17 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
      * fp32: M <= 16, W stored N x K or K x N, fp32 output.  vkb_skinny_plan holds the
      * kernels' own limits (leading dimensions, 32-bit buffer spans) and
      * returns their K split, or 0: then a tile path. */
-    /* 16-bit, 41-64 rows, K >= 4096 and at most 128 column tiles of 128:
-     * the short-M pipelined tiles with a K split (below) beat the decode
-     * kernels.  fp16, one box: N = 14336 / 11008 / 4096, K = 4096, M = 64
-     * 34.6 / 32.6 / 17.7 -> 26.4 / 22.4 / 14.3 us, M = 41 30.0 / 27.0 / 14.1 ->
-     * 25.7 / 21.0 / 13.1; 8192^2 M = 64 32.5 -> 27.9 (weight K x N 35.4 ->
-     * 29.1).  With more column tiles (N = 28672, unsplit tiles) the decode
-     * kernels stay ahead (92.6 against 108.1 us). */
-    const int tiles_first = ab_type != VKBLAS_DT_F32 && M > 40 && K >= 4096 && split_k == 0 && batch == 1 &&
+    /* 16-bit, 33-64 rows (25-64 against N >= 8192), K >= 4096 and at most
+     * 128 column tiles of 128: the short-M pipelined tiles with a K split
+     * (below) beat the decode kernels.  fp16, one box: N = 14336 / 11008 /
+     * 4096, K = 4096, M = 64 34.6 / 32.6 / 17.7 -> 26.4 / 22.4 / 14.3 us,
+     * M = 40 29.7 / 27.0 / 13.7 -> 25.1 / 21.3 / 12.4, M = 24 24.6 / 22.1 /
+     * 11.6 -> 24.0 / 20.9 / 11.8; 8192^2 M = 64 32.5 -> 27.9 (weight K x N
+     * 35.4 -> 29.1), M = 24 27.8 -> 25.3.  With more column tiles (N =
+     * 28672, unsplit tiles) the decode kernels stay ahead (92.6 against
+     * 108.1 us at 64 rows). */
+    const int tiles_first = ab_type != VKBLAS_DT_F32 && M > (N >= 8192 ? 24u : 32u) && K >= 4096 && split_k == 0 &&
+                            batch == 1 &&
                             g_force_tile < 0 && cdiv(N, 128) <= 128 &&
                             pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned);
     if (op_a == VKBLAS_OP_N && batch == 1 && split_k <= 1 && aligned && !g_no_skinny && !tiles_first &&
