@@ -261,8 +261,9 @@ def test_plan_decode_split():
 
 
 def test_plan_skinny_f32():
-    """fp32 with up to 16 activation rows (op_a = N, fp32 output): the skinny
-    kernels for W stored N x K (op_b = T, no split) and K x N (op_b = N, N a
+    """fp32 activation rows (op_a = N, fp32 output): the skinny kernels for up
+    to 16 rows against W stored N x K (op_b = T, no split), the decode kernel
+    for 17-64 rows against N x K, and K x N (op_b = N, M <= 16, N a
     multiple of 4, K split in whole 64-row groups so that the grid holds at
     most 256 workgroups of 128 columns, each slice at least 4 groups)."""
     for M in (1, 2, 4, 9, 16):
@@ -275,9 +276,15 @@ def test_plan_skinny_f32():
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 1024, 65536, 65536, 1024, 1024).split == 32
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 3, 8192, 1000, 1000, 8192, 8192).split == 4
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 1, 4, 1, 4, 4, 4).split == 1
-    # not skinny: 17 rows, 16-bit output, N % 4 (K x N), op_a = T, misaligned
-    # leading dimensions, ldb short of N
-    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    # 17-64 rows against W stored N x K: the decode kernel, K split in
+    # 64-float steps (8192^2: 64 workgroups of 128 rows x 4 slices)
+    for M in (17, 40, 64):
+        pl = P(vk.DT_F32, vk.DT_F32, 0, 1, M, 8192, 8192, 8192, 8192, 8192)
+        assert pl.path == vk.PATH_SKINNY and pl.split == 4, (M, pl.path, pl.split)
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    # not skinny: 17 rows against K x N, 16-bit output, N % 4 (K x N), op_a = T,
+    # misaligned leading dimensions, ldb short of N
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8190, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F32, 1, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
@@ -336,9 +343,11 @@ def test_plan_split_mid_size_m():
             assert (pl(65).path, pl(65).split, pl(65).tile) == (vk.PATH_SPLITK, 4, 1)        # short M, 64 tiles
             assert pl(384).split == 1 and pl(384).path != vk.PATH_SPLITK                     # 192 tiles
             assert pl(128, K=2048).split == 1                                                # K below 4096
-    # fp32 from 17 to 64 rows and short M with MN-major A: the generic kernel
-    pl = P(vk.DT_F32, vk.DT_F32, 0, 1, 64, 4096, 4096, 4096, 4096, 4096)
+    # fp32 from 17 to 64 rows against W stored K x N and short M with MN-major
+    # A: the generic kernel (against W stored N x K: the decode kernel)
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 64, 4096, 4096, 4096, 4096, 4096)
     assert pl.path in (vk.PATH_SPLITK, vk.PATH_TILE64) and pl.tile == 0
+    assert P(vk.DT_F32, vk.DT_F32, 0, 1, 64, 4096, 4096, 4096, 4096, 4096).path == vk.PATH_SKINNY
     pl = P(vk.DT_F16, vk.DT_F16, 1, 1, 96, 8192, 8192, 96, 8192, 8192)
     assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 8, 1)
     assert P(vk.DT_F16, vk.DT_F16, 0, 0, 1024, 1024, 8192, 8192, 1024, 1024).split == 4

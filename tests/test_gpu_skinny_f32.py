@@ -1,10 +1,12 @@
-"""The fp32 skinny kernels (engine op_a = N, M <= 16 activation rows, fp32
-output), the path of the reference's fp32 matvec (src/vkblas.c:2100-2143,
-2501-2607; shaders/matvec_f32_tmpl.comp:23-74, TB = 0 and TB = 1):
+"""The fp32 skinny kernels (engine op_a = N, fp32 output), the path of the
+reference's fp32 matvec (src/vkblas.c:2100-2143, 2501-2607;
+shaders/matvec_f32_tmpl.comp:23-74, TB = 0 and TB = 1):
 
-  op_b = T: W stored N x K (each output's K weights contiguous), the staged
-            MFMA skinny kernel with 16-byte fragments of 4 floats;
-  op_b = N: W stored K x N (N-contiguous rows), the K x N MFMA kernel, with
+  op_b = T: W stored N x K (each output's K weights contiguous), up to 64
+            activation rows: the staged MFMA skinny kernel with 16-byte
+            fragments of 4 floats (M <= 16), the staged decode kernel with
+            a K split over the grid (17 <= M <= 64);
+  op_b = N: W stored K x N (N-contiguous rows), M <= 16: the K x N MFMA kernel, with
             a K split over the grid for long K (fp32 partials + the
             fixed-order reduce).
 
@@ -41,6 +43,15 @@ CASES_T += [
     (16, 8192, 520, 0, 0, 0, 0.5),
     (10, 8240, 3000, 4, 0, 0, 0.5),      # two tiles, two waves, three stages over 46 K steps
     (16, 64, 13, 3, 3, 2, -0.5),
+    # 17-64 rows: the decode kernel, 64-float K steps, ragged last step
+    (17, 1000, 1028, 0, 0, 0, 0.0),
+    (20, 64, 13, 3, 3, 2, -0.5),         # no full step: the checked tail only
+    (24, 300, 4100, 4, 4, 1, 0.5),       # K split, the last slice ending in a partial step
+    (32, 4096, 4096, 0, 0, 0, 0.0),      # two weight tiles per wave, K split
+    (33, 257, 2051, 1, 1, 0, -0.5),      # three activation tiles, the last one row
+    (48, 8192, 1000, 0, 4, 0, 0.0),
+    (64, 4096, 4100, 4, 0, 3, 0.25),
+    (64, 129, 64, 0, 0, 0, 0.0),         # one full step, unsplit
 ]
 
 CASES_N = []
@@ -144,6 +155,15 @@ def test_skinny_f32_epilogue(op_b, M, N, K, beta, sep):
     _run((M, N, K, 4, 4, 4, beta), op_b, ex={"sep": sep})
 
 
+@pytest.mark.parametrize("M,N,K", [(17, 1000, 4100), (40, 1000, 252), (64, 520, 4100)])
+@pytest.mark.parametrize("beta,sep", [(0.0, False), (0.5, False), (-0.75, True)])
+def test_decode_f32_epilogue(M, N, K, beta, sep):
+    """17-64 rows against W stored N x K: bias and C_in applied by the decode
+    kernel (K = 252, unsplit) or once by the reduce after its K split"""
+    print(f"[case] fp32 decode epilogue M={M} N={N} K={K} beta={beta} sep={sep}", flush=True)
+    _run((M, N, K, 4, 4, 4, beta), 1, ex={"sep": sep})
+
+
 @pytest.mark.parametrize("op_b", [0, 1])
 @pytest.mark.parametrize("M", [1, 7, 16])
 def test_skinny_f32_device_scalars(op_b, M):
@@ -176,7 +196,7 @@ def test_skinny_f32_deterministic():
     from gpu_helpers import to_dev, to_host
     print("[case] fp32 skinny determinism", flush=True)
     for op_b, M, N, K in ((1, 1, 4096, 8192), (1, 16, 8192, 1024), (0, 1, 8192, 8192), (0, 16, 4096, 14336),
-                          (0, 3, 1000, 100)):
+                          (0, 3, 1000, 100), (1, 40, 4096, 4096), (1, 64, 1000, 4100)):
         ldb = K if op_b else N
         dX = to_dev(_padded(M, K, K, 21, 1.0))
         dW = to_dev(_padded(N, K, K, 22, 0.05) if op_b else _padded(K, N, N, 22, 0.05))

@@ -1,4 +1,4 @@
-// skinny.hip — bandwidth-bound fp16 / bf16 skinny GEMM / matvec for decode.
+// skinny.hip — bandwidth-bound skinny GEMM / matvec for decode (fp16, bf16, fp32).
 //
 // Replaces the reference's matvec family (src/vkblas.c:2100-2392, 2501-2808;
 // shaders matvec_splitk_tmpl.comp, matvec_splitk_m_tmpl.comp and the
@@ -15,9 +15,9 @@
 //  * 3 <= M <= 16: skinny_lds_kernel, one v_mfma_f32_16x16x32_{f16,bf16}
 //    tile (src A = 16 weight rows, src B = up to 16 activation rows) whose
 //    operands are copied to LDS as whole lines and read back as fragments;
-//  * 17 <= M <= 64: decode_lds_kernel, weights and activations copied to
-//    a shared LDS stage as whole lines (activations read from L2 once per
-//    128 weight rows), K split over the grid.
+//  * 17 <= M <= 64: decode_lds_kernel (16-bit types and fp32), weights and
+//    activations copied to a shared LDS stage as whole lines (activations
+//    read from L2 once per 128 weight rows), K split over the grid.
 // Lane group g = lane / 16 of MFMA j takes k in [32 j + 8 g, +8) of a step:
 // the same k for both operands, every k exactly once.  Partial tiles are
 // summed in a fixed order (deterministic), then alpha / beta are applied once.
@@ -111,8 +111,9 @@ struct DecPlan {
     int r;
     uint32_t split;
 };
-__host__ __device__ inline DecPlan dec_plan(uint32_t N, uint32_t K) {
-    const uint32_t nsteps = (K + 127) / 128;
+__host__ __device__ inline DecPlan dec_plan(uint32_t N, uint32_t K, uint32_t es) {
+    const uint32_t ks = 256 / es;   // k per step
+    const uint32_t nsteps = (K + ks - 1) / ks;
     auto split_for = [&](uint32_t wg, uint32_t round) {
         uint32_t sp = round / (wg ? wg : 1);
         if (sp > nsteps / 4) sp = nsteps / 4;
@@ -475,13 +476,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(SkParams p) {
 }
 
 // ------------------------------------------------------- staged decode
-// For 17 <= M <= 64 activation rows.  The workgroup owns 64 R weight rows
+// For 17 <= M <= 64 activation rows, fp16 / bf16 or fp32.  The workgroup owns 64 R weight rows
 // (wave w computes rows 16 R w .. 16 R w + 16 R - 1: R 16-row tiles, R = 1
 // or 2, see dec_plan) against all 16 MT activation rows (MT = ceil(M / 16)
 // tiles), and the grid splits K
 // over blockIdx.y: with nsplit > 1 each workgroup writes raw fp32 partials
 // (part + split * M * N, row pitch N) that splitk_reduce sums in split order.
-// Per 128-wide K step the workgroup copies its weight rows and the
+// Per K step (256 bytes of each row: 128 k of a 16-bit type, one
+// v_mfma_f32_16x16x32 per fragment; 64 k of fp32, four v_mfma_f32_16x16x4f32
+// per fragment, see mfma_frag) the workgroup copies its weight rows and the
 // activation rows into one shared LDS stage as whole 256-byte row pieces
 // (buffer_load_dwordx4 ... lds, 4 rows per instruction; wave w copies its own
 // weight rows and a quarter of the activation rows), S stages, S - 1 steps in
@@ -503,10 +506,11 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, g = lane >> 4;
     const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
-    const uint16_t* pX = (const uint16_t*)p.X;
-    const uint16_t* pW = (const uint16_t*)p.W;
+    constexpr int ES = (int)sizeof(T), KS = 256 / ES;        // element bytes, k per step
+    const T* pX = (const T*)p.X;
+    const T* pW = (const T*)p.W;
     const int wrow0 = blockIdx.x * WROWS + wave * 16 * R;     // this wave's first weight row
-    const int nsteps = (K + 127) / 128, full_steps = K / 128;
+    const int nsteps = (K + KS - 1) / KS, full_steps = K / KS;
     const int per = (nsteps + nsplit - 1) / nsplit;
     const int s_beg = (int)blockIdx.y * per;
     const int s_end = min(nsteps, s_beg + per);
@@ -523,18 +527,18 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
     // the read domain of the rows it copies
     const int wbase = min(wrow0, N - 1);
     const int wlast = min(wrow0 + 16 * R - 1, N - 1);
-    const i32x4 rw = rsrc_words(pW + (int64_t)wbase * p.ldb, ((int64_t)(wlast - wbase) * p.ldb + K) * 2);
-    const i32x4 rx = rsrc_words(pX, ((int64_t)(M - 1) * p.lda + K) * 2);
+    const i32x4 rw = rsrc_words(pW + (int64_t)wbase * p.ldb, ((int64_t)(wlast - wbase) * p.ldb + K) * ES);
+    const i32x4 rx = rsrc_words(pX, ((int64_t)(M - 1) * p.lda + K) * ES);
     int vw[4 * R], vx[MT];
 #pragma unroll
     for (int q = 0; q < 4 * R; ++q) {
         const int rr = 4 * q + g;                               // row within the wave's 16 R
-        vw[q] = (int)((int64_t)(min(wrow0 + rr, N - 1) - wbase) * p.ldb * 2) + ((l16 ^ (rr & 15)) << 4);
+        vw[q] = (int)((int64_t)(min(wrow0 + rr, N - 1) - wbase) * p.ldb * ES) + ((l16 ^ (rr & 15)) << 4);
     }
 #pragma unroll
     for (int q = 0; q < MT; ++q) {
         const int xr = wave * 4 * MT + 4 * q + g;               // activation row
-        vx[q] = (int)((int64_t)min(xr, M - 1) * p.lda * 2) + ((l16 ^ (xr & 15)) << 4);
+        vx[q] = (int)((int64_t)min(xr, M - 1) * p.lda * ES) + ((l16 ^ (xr & 15)) << 4);
     }
     // the workgroups of a K slice walk it from rotated starts, so they do
     // not all read the same column range of their rows at once
@@ -591,16 +595,16 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wf[r][j], xf[t][j], acc[r][t]);
+                for (int t = 0; t < MT; ++t) acc[r][t] = mfma_frag<T>(wf[r][j], xf[t][j], acc[r][t]);
         stage = stage + 1 == S ? 0 : stage + 1;
     }
     if (tail) {   // partial last K step, zero-filled beyond K
-        const int kb = full_steps * 128;
+        const int kb = full_steps * KS;
         const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
         u32x4 wt[R][4], xt[MT][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int k = kb + 32 * j + 8 * g;
+            const int k = kb + (KS / 4) * j + (16 / ES) * g;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = wrow0 + 16 * r + l16;
@@ -617,7 +621,7 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 #pragma unroll
             for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) acc[r][t] = mfma16<T>(wt[r][j], xt[t][j], acc[r][t]);
+                for (int t = 0; t < MT; ++t) acc[r][t] = mfma_frag<T>(wt[r][j], xt[t][j], acc[r][t]);
     }
 
     // D row 4 g + e = weight row, column l16 = activation row: each lane
@@ -1057,7 +1061,7 @@ int launch_dec_r(const SkParams& p, float* part, int nsplit, hipStream_t st) {
 
 template <typename T, typename TC>
 int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
-    return dec_plan(p.N, p.K).r == 2 ? launch_dec_r<T, TC, 2>(p, part, nsplit, st)
+    return dec_plan(p.N, p.K, sizeof(T)).r == 2 ? launch_dec_r<T, TC, 2>(p, part, nsplit, st)
                                      : launch_dec_r<T, TC, 1>(p, part, nsplit, st);
 }
 
@@ -1154,8 +1158,8 @@ extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint3
     const int64_t vec = 16 / es;
     if ((M > 1 && (lda % vec || lda < (int64_t)K)) || ldb % vec) return 0;
     if (ab_type == VKB_T_F32) {
-        if (M > 16) return 0;
-        if (!b_kmajor) return (N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(N, K).split;
+        if (!b_kmajor) return (M > 16 || N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(N, K).split;
+        if (M > 64) return 0;
     } else if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) {
         return 0;
     } else if (!b_kmajor) {
@@ -1170,8 +1174,8 @@ extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint3
     if (ldb < (int64_t)K || (uint64_t)32 * ldb * es >= (1ull << 31) ||
         ((xrows - 1) * (uint64_t)lda + K) * es >= (1ull << 31))
         return 0;
-    if (ab_type == VKB_T_F32 || (int)M < DEC_MIN_M) return 1;
-    return dec_plan(N, K).split;
+    if ((int)M < DEC_MIN_M) return 1;
+    return dec_plan(N, K, (uint32_t)es).split;
 }
 
 extern "C" int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64_t lda, const void* W, int64_t ldb,
@@ -1202,6 +1206,7 @@ extern "C" int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64
     const bool f32_out = c_type == VKB_T_F32;
     if (ab_type == VKB_T_F32) {
         if (!b_kmajor) return launch_skn<float>(p, part, nsplit, st);
+        if ((int)p.M >= DEC_MIN_M) return launch_dec_mt<float, float>(p, part, (int)nsplit, st);
         return launch_sk_lds<float, float>(p, st);
     }
     if (!b_kmajor) {
