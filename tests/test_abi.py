@@ -134,10 +134,10 @@ def test_plan_rejects_bad_arguments():
         P(vk.DT_F16, vk.DT_BF16, 0, 0, 4, 4, 4, 4, 4, 4)         # f16 in, bf16 out: unsupported
     with pytest.raises(vk.VkblasError):
         P(vk.DT_BF16, vk.DT_F16, 0, 0, 4, 4, 4, 4, 4, 4)         # bf16 in, f16 out: unsupported
-    # fp32 in, 16-bit out (GemmEx 32F/32F/16F and 16BF): a tile path (20
+    # fp32 in, 16-bit out (GemmEx 32F/32F/16F and 16BF): a tile path (80
     # rows: more than the fp32 skinny kernels take)
     for ct in (vk.DT_F32, vk.DT_F16, vk.DT_BF16):
-        assert P(vk.DT_F32, ct, 0, 0, 20, 4, 4, 4, 4, 4).path == vk.PATH_TILE64
+        assert P(vk.DT_F32, ct, 0, 0, 80, 4, 4, 4, 4, 4).path == vk.PATH_TILE64
 
 
 def test_engine_param_errors_without_gpu():
@@ -282,9 +282,14 @@ def test_plan_skinny_f32():
         pl = P(vk.DT_F32, vk.DT_F32, 0, 1, M, 8192, 8192, 8192, 8192, 8192)
         assert pl.path == vk.PATH_SKINNY and pl.split == 4, (M, pl.path, pl.split)
     assert P(vk.DT_F32, vk.DT_F32, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
-    # not skinny: 17 rows against K x N, 16-bit output, N % 4 (K x N), op_a = T,
-    # misaligned leading dimensions, ldb short of N
-    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 17, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    # 17-64 rows against K x N: workgroups of 64 columns (8192^2: 128 of them
+    # x 2 slices of 64 groups)
+    for M in (17, 40, 64):
+        pl = P(vk.DT_F32, vk.DT_F32, 0, 0, M, 8192, 8192, 8192, 8192, 8192)
+        assert pl.path == vk.PATH_SKINNY and pl.split == 2, (M, pl.path, pl.split)
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
+    # not skinny: 16-bit output, N % 4 (K x N), op_a = T, misaligned leading
+    # dimensions, ldb short of N
     assert P(vk.DT_F32, vk.DT_F16, 0, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8190, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F32, 1, 1, 4, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
@@ -343,10 +348,9 @@ def test_plan_split_mid_size_m():
             assert (pl(65).path, pl(65).split, pl(65).tile) == (vk.PATH_SPLITK, 4, 1)        # short M, 64 tiles
             assert pl(384).split == 1 and pl(384).path != vk.PATH_SPLITK                     # 192 tiles
             assert pl(128, K=2048).split == 1                                                # K below 4096
-    # fp32 from 17 to 64 rows against W stored K x N and short M with MN-major
-    # A: the generic kernel (against W stored N x K: the decode kernel)
-    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 64, 4096, 4096, 4096, 4096, 4096)
-    assert pl.path in (vk.PATH_SPLITK, vk.PATH_TILE64) and pl.tile == 0
+    # fp32 from 17 to 64 rows: the decode kernels, W stored either way; short
+    # M with MN-major A: the pipelined tiles with a K split
+    assert P(vk.DT_F32, vk.DT_F32, 0, 0, 64, 4096, 4096, 4096, 4096, 4096).path == vk.PATH_SKINNY
     assert P(vk.DT_F32, vk.DT_F32, 0, 1, 64, 4096, 4096, 4096, 4096, 4096).path == vk.PATH_SKINNY
     pl = P(vk.DT_F16, vk.DT_F16, 1, 1, 96, 8192, 8192, 96, 8192, 8192)
     assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 8, 1)
@@ -404,10 +408,13 @@ def test_plan_split_heuristic_and_off():
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 64 == 0 and 4 * pl.split <= 256
     # below the tile in M: from 65 rows (K-major A) the pipelined 128x128
-    # pass 1 (rows past M read as row M - 1), up to 64 rows the generic 64x64
+    # pass 1 (rows past M read as row M - 1); up to 64 rows the decode kernel
+    # (K-major A) or the generic 64x64 (MN-major A)
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 100, 256, 65536, 65536, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 1 and pl.k_per_split % 64 == 0
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 60, 256, 65536, 65536, 256, 256)
+    assert pl.path == vk.PATH_SKINNY and pl.split == 64
+    pl = P(vk.DT_F32, vk.DT_F32, 1, 0, 60, 256, 65536, 60, 256, 256)
     assert pl.path == vk.PATH_SPLITK and pl.tile == 0
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=1)
     assert pl.path != vk.PATH_SPLITK

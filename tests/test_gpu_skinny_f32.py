@@ -6,7 +6,7 @@ shaders/matvec_f32_tmpl.comp:23-74, TB = 0 and TB = 1):
             activation rows: the staged MFMA skinny kernel with 16-byte
             fragments of 4 floats (M <= 16), the staged decode kernel with
             a K split over the grid (17 <= M <= 64);
-  op_b = N: W stored K x N (N-contiguous rows), M <= 16: the K x N MFMA kernel, with
+  op_b = N: W stored K x N (N-contiguous rows), up to 64 rows: the K x N MFMA kernel, with
             a K split over the grid for long K (fp32 partials + the
             fixed-order reduce).
 
@@ -70,6 +70,15 @@ CASES_N += [
     (16, 260, 33, 3, 4, 4, 0.5),         # two full chunks and a 1-row partial one
     (5, 516, 20, 0, 0, 0, -0.5),         # one full chunk and a partial one; 5 column blocks
     (8, 252, 4096, 0, 4, 0, 0.0),        # the second 128-column block partial
+    # 17-64 rows: four waves along K, one 64-column group, 2-4 activation tiles
+    (17, 1000, 1028, 0, 0, 0, 0.0),
+    (20, 68, 13, 3, 4, 2, -0.5),         # one partial chunk only; the second column group partial
+    (24, 300, 4100, 4, 4, 1, 0.5),       # K split
+    (32, 4096, 4096, 0, 0, 0, 0.0),
+    (33, 260, 2051, 1, 8, 0, -0.5),      # the third activation tile one row
+    (48, 8192, 1000, 0, 4, 0, 0.0),
+    (64, 4096, 4100, 4, 0, 3, 0.25),
+    (64, 132, 64, 0, 0, 0, 0.0),         # four chunks, unsplit
 ]
 
 
@@ -155,13 +164,14 @@ def test_skinny_f32_epilogue(op_b, M, N, K, beta, sep):
     _run((M, N, K, 4, 4, 4, beta), op_b, ex={"sep": sep})
 
 
+@pytest.mark.parametrize("op_b", [0, 1])
 @pytest.mark.parametrize("M,N,K", [(17, 1000, 4100), (40, 1000, 252), (64, 520, 4100)])
 @pytest.mark.parametrize("beta,sep", [(0.0, False), (0.5, False), (-0.75, True)])
-def test_decode_f32_epilogue(M, N, K, beta, sep):
-    """17-64 rows against W stored N x K: bias and C_in applied by the decode
-    kernel (K = 252, unsplit) or once by the reduce after its K split"""
-    print(f"[case] fp32 decode epilogue M={M} N={N} K={K} beta={beta} sep={sep}", flush=True)
-    _run((M, N, K, 4, 4, 4, beta), 1, ex={"sep": sep})
+def test_decode_f32_epilogue(op_b, M, N, K, beta, sep):
+    """17-64 rows: bias and C_in applied by the kernel (K = 252, unsplit) or
+    once by the reduce after its K split"""
+    print(f"[case] fp32 decode epilogue op_b={op_b} M={M} N={N} K={K} beta={beta} sep={sep}", flush=True)
+    _run((M, N, K, 4, 4, 4, beta), op_b, ex={"sep": sep})
 
 
 @pytest.mark.parametrize("op_b", [0, 1])
@@ -196,7 +206,8 @@ def test_skinny_f32_deterministic():
     from gpu_helpers import to_dev, to_host
     print("[case] fp32 skinny determinism", flush=True)
     for op_b, M, N, K in ((1, 1, 4096, 8192), (1, 16, 8192, 1024), (0, 1, 8192, 8192), (0, 16, 4096, 14336),
-                          (0, 3, 1000, 100), (1, 40, 4096, 4096), (1, 64, 1000, 4100)):
+                          (0, 3, 1000, 100), (1, 40, 4096, 4096), (1, 64, 1000, 4100), (0, 40, 4096, 4096),
+                          (0, 64, 1000, 4100)):
         ldb = K if op_b else N
         dX = to_dev(_padded(M, K, K, 21, 1.0))
         dW = to_dev(_padded(N, K, K, 22, 0.05) if op_b else _padded(K, N, N, 22, 0.05))

@@ -356,7 +356,8 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
      * fp16 / bf16: M <= 64, W stored N x K (op_b = T) or K x N (op_b = N);
      * fp32, fp32 output: M <= 64 with W stored N x K (17-64 rows: the decode
      * kernel; 17-32 rows against 14336 x 4096 52 us where the tile paths
-     * took 160, 4096 x 4096 20 against 48), M <= 16 with W K x N.  At exactly 64
+     * took 160, 4096 x 4096 20 against 48), M <= 64 with W K x N (17-32 rows
+     * 14336 x 4096 56-58 against 242-244 us).  At exactly 64
      * rows the tile paths are within -8 .. +11 % of it; at 48 rows they are
      * 1.6-2.2x slower (edge rows).  vkb_skinny_plan holds the
      * kernels' own limits (leading dimensions, 32-bit buffer spans) and

@@ -660,7 +660,7 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 }
 
 // ------------------------------------------------ fp32, W stored K x N
-// C[m][n] = alpha * sum_k X[m][k] * W[k][n] + ...,  M <= 16, each W row
+// C[m][n] = alpha * sum_k X[m][k] * W[k][n] + ...,  M <= 64, each W row
 // N-contiguous: the reference's TB = 0 matvec (matvec_f32_tmpl.comp:27-58,
 // four contiguous columns per thread), here on the matrix cores.  One
 // v_mfma_f32_16x16x4_f32 takes 4 k of 16 activation rows (A operand: lane
@@ -674,7 +674,8 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 // e taking k = k0 + 4 g + e: lane group g loads W rows k0 + 4 g .. + 3 and
 // X[l16][k0 + 4 g .. + 3] (one 16-byte load).  Tile c's D[i][j] sits in lane
 // (j, i / 4), component i % 4, so lane (l16, g) owns C[4 g + r][nl .. nl + 3]:
-// one 16-byte store per activation row.
+// one 16-byte store per activation row.  MT activation tiles (rows 16 t ..
+// 16 t + 15, M up to 16 MT) share each W fragment: acc[t][c].
 // Workgroup: WV waves, WV / KW column groups of 64 side by side, KW waves
 // along K splitting the workgroup's slice into contiguous parts whose sums
 // are added in LDS in wave order.  Each wave loads the next chunk while it
@@ -682,25 +683,31 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 // (PARTIAL: fp32 partials for the fixed-order reduce); the plan keeps the
 // grid to one round of at most 256 workgroups, one per CU (measured on
 // 8192x8192, 4096x14336 and 14336x4096: 0.74-0.82 of HBM; 384-512
-// workgroups, two per CU, 0.58-0.71).
+// workgroups, two per CU, 0.58-0.71).  17-64 rows: four waves along K, one
+// column group (the LDS sums and accumulators grow with MT); against the
+// tile paths (same box, 17 / 32 / 64 rows) 14336 x 4096 56 / 58 / 85 us
+// against 242 / 244 / 108, 8192^2 58 / 60 / 88 against 157 / 167 / 95.
 // Requires N % 4 == 0 (lanes past N load the last 4 columns and store
 // nothing), ldb % 4 == 0, lda % 4 == 0 (or M == 1) and 16-byte aligned X, W.
 // Activation rows past M load row M - 1 (their outputs are dropped); k past
 // K in the last chunk is zero in both operands.
 constexpr int SKN_WV = 8, SKN_KW = 4;
-constexpr int SKN_COLS = 64 * SKN_WV / SKN_KW;   // columns per workgroup
+constexpr int SKN_COLS = 64 * SKN_WV / SKN_KW;   // columns per workgroup, M <= 16
+constexpr int SKN_COLS_MT = 64;                  // 17 <= M <= 64: four waves along K
 
-template <typename TC, int WV, int KW, bool PARTIAL>
+template <typename TC, int WV, int KW, int MT, bool PARTIAL>
 __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* part, int per) {
     constexpr int CG = WV / KW;                  // column groups of 64 per workgroup
-    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * 4 * 64 : 1];
+    __shared__ floatx4 red[KW > 1 ? (KW - 1) * CG * 4 * MT * 64 : 1];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int cg = wave % CG, kw = wave / CG;
     const int l16 = lane & 15, g = lane >> 4;
     const int N = (int)p.N, M = (int)p.M, K = (int)p.K;
     const int nl = blockIdx.x * (64 * CG) + cg * 64 + 4 * l16;   // this lane's columns
     const float* W = (const float*)p.W + min(nl, N - 4);
-    const float* X = (const float*)p.X + (int64_t)min(l16, M - 1) * p.lda;
+    const float* X[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) X[t] = (const float*)p.X + (int64_t)min(16 * t + l16, M - 1) * p.lda;
     const int64_t ldb = p.ldb;
     const int chunks = (K + 15) / 16;
     const int s_beg = (int)blockIdx.y * per;                      // the workgroup's slice
@@ -710,27 +717,32 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
     const int c_end = min(s_end, c_beg + sub);
     const int f_end = max(c_beg, min(c_end, K / 16));             // chunks with 16 valid k
 
-    floatx4 acc[4];
+    floatx4 acc[MT][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) acc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-    auto load = [&](int ch, floatx4 (&w)[4], floatx4& x) {
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][c] = floatx4{0.f, 0.f, 0.f, 0.f};
+    auto load = [&](int ch, floatx4 (&w)[4], floatx4 (&x)[MT]) {
         const int64_t k = (int64_t)ch * 16 + 4 * g;
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[e] = __builtin_nontemporal_load((const floatx4*)(W + (k + e) * ldb));
-        x = *(const floatx4*)(X + k);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) x[t] = *(const floatx4*)(X[t] + k);
     };
-    auto mma = [&](const floatx4 (&w)[4], const floatx4& x) {
+    auto mma = [&](const floatx4 (&w)[4], const floatx4 (&x)[MT]) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[e], w[e][c], acc[c], 0, 0, 0);
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[t][e], w[e][c], acc[t][c], 0, 0, 0);
     };
     // full chunks, the next chunk's loads in flight
     const int nf = f_end - c_beg;
     int ch = c_beg;
     {
-        floatx4 wa[4], xa, wb[4], xb;
+        floatx4 wa[4], xa[MT], wb[4], xb[MT];
         int i = 0;
         if (nf > 0) load(ch, wa, xa);
         for (; i + 1 < nf; i += 2) {
@@ -748,12 +760,13 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
     // the partial last chunk, k past K zero
     for (; ch < c_end; ++ch) {
         const int k = ch * 16 + 4 * g;
-        floatx4 w[4], x;
+        floatx4 w[4], x[MT];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const bool ok = k + e < K;
             w[e] = ok ? *(const floatx4*)(W + (int64_t)(k + e) * ldb) : floatx4{0.f, 0.f, 0.f, 0.f};
-            x[e] = ok ? X[k + e] : 0.f;
+#pragma unroll
+            for (int t = 0; t < MT; ++t) x[t][e] = ok ? X[t][k + e] : 0.f;
         }
         mma(w, x);
     }
@@ -761,25 +774,31 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
     if constexpr (KW > 1) {
         if (kw > 0) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) red[(((kw - 1) * CG + cg) * 4 + c) * 64 + lane] = acc[c];
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) red[((((kw - 1) * CG + cg) * MT + t) * 4 + c) * 64 + lane] = acc[t][c];
         }
         __syncthreads();
         if (kw > 0) return;
 #pragma unroll
         for (int j = 1; j < KW; ++j)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] += red[(((j - 1) * CG + cg) * 4 + c) * 64 + lane];
+            for (int t = 0; t < MT; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[t][c] += red[((((j - 1) * CG + cg) * MT + t) * 4 + c) * 64 + lane];
     }
 
     if (nl >= N) return;
     if constexpr (PARTIAL) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            if (m < M)
-                *(floatx4*)(part + ((int64_t)blockIdx.y * M + m) * N + nl) =
-                    floatx4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-        }
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * t + 4 * g + r;
+                if (m < M)
+                    *(floatx4*)(part + ((int64_t)blockIdx.y * M + m) * N + nl) =
+                        floatx4{acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]};
+            }
     } else {
         float alpha = p.alpha, beta = p.beta;
         if (p.mode == 1) {
@@ -792,19 +811,21 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
         float b4[4] = {0.f, 0.f, 0.f, 0.f};
         vkb::add_bias4(p.epi, nl, 4, b4);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = 4 * g + r;
-            if (m >= M) continue;
-            TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
-            const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+        for (int t = 0; t < MT; ++t)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                float y = alpha * acc[c][r];
-                if (beta != 0.0f) y += beta * (float)src[c];
-                if (p.epi.bias) y += b4[c];
-                dst[c] = (TC)y;
+            for (int r = 0; r < 4; ++r) {
+                const int m = 16 * t + 4 * g + r;
+                if (m >= M) continue;
+                TC* dst = (TC*)p.C + (int64_t)m * p.ldc + nl;
+                const TC* src = (const TC*)p.epi.cin + (int64_t)m * p.epi.ldcin + nl;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float y = alpha * acc[t][c][r];
+                    if (beta != 0.0f) y += beta * (float)src[c];
+                    if (p.epi.bias) y += b4[c];
+                    dst[c] = (TC)y;
+                }
             }
-        }
     }
 }
 
@@ -1090,8 +1111,9 @@ int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipSt
 struct SknPlan {
     uint32_t split, per;
 };
-inline SknPlan skn_plan(uint32_t N, uint32_t K) {
-    const uint32_t wg = (N + SKN_COLS - 1) / SKN_COLS;
+inline SknPlan skn_plan(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t cols = M <= 16 ? SKN_COLS : SKN_COLS_MT;
+    const uint32_t wg = (N + cols - 1) / cols;
     const uint32_t groups = (K + 63) / 64;
     uint32_t sp = 256 / wg;
     if (sp > groups / 4) sp = groups / 4;
@@ -1101,14 +1123,27 @@ inline SknPlan skn_plan(uint32_t N, uint32_t K) {
     return SknPlan{(groups + gper - 1) / gper, 4 * gper};
 }
 
+template <typename TC, int WV, int MT>
+void launch_skn_mt(const SkParams& p, float* part, uint32_t nsplit, int per, hipStream_t st) {
+    constexpr int cols = 64 * WV / SKN_KW;
+    const dim3 grid((p.N + cols - 1) / cols, nsplit), block(64 * WV);
+    if (nsplit > 1)
+        hipLaunchKernelGGL((skinny_n_kernel<float, WV, SKN_KW, MT, true>), grid, block, 0, st, p, part, per);
+    else
+        hipLaunchKernelGGL((skinny_n_kernel<TC, WV, SKN_KW, MT, false>), grid, block, 0, st, p, part, per);
+}
+
+// up to 16 rows: eight waves (two column groups of 64); 17-64 rows: four
+// waves, one column group, 2-4 activation tiles
 template <typename TC>
 int launch_skn(const SkParams& p, float* part, uint32_t nsplit, hipStream_t st) {
-    const SknPlan pl = skn_plan(p.N, p.K);
-    const dim3 grid((p.N + SKN_COLS - 1) / SKN_COLS, nsplit), block(64 * SKN_WV);
-    if (nsplit > 1)
-        hipLaunchKernelGGL((skinny_n_kernel<float, SKN_WV, SKN_KW, true>), grid, block, 0, st, p, part, (int)pl.per);
-    else
-        hipLaunchKernelGGL((skinny_n_kernel<TC, SKN_WV, SKN_KW, false>), grid, block, 0, st, p, part, (int)pl.per);
+    const int per = (int)skn_plan(p.M, p.N, p.K).per;
+    switch ((p.M + 15) / 16) {
+        case 1: launch_skn_mt<TC, SKN_WV, 1>(p, part, nsplit, per, st); break;
+        case 2: launch_skn_mt<TC, 4, 2>(p, part, nsplit, per, st); break;
+        case 3: launch_skn_mt<TC, 4, 3>(p, part, nsplit, per, st); break;
+        default: launch_skn_mt<TC, 4, 4>(p, part, nsplit, per, st); break;
+    }
     return (int)hipGetLastError();
 }
 
@@ -1158,7 +1193,7 @@ extern "C" uint32_t vkb_skinny_plan(int ab_type, int b_kmajor, uint32_t M, uint3
     const int64_t vec = 16 / es;
     if ((M > 1 && (lda % vec || lda < (int64_t)K)) || ldb % vec) return 0;
     if (ab_type == VKB_T_F32) {
-        if (!b_kmajor) return (M > 16 || N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(N, K).split;
+        if (!b_kmajor) return (M > 64 || N % 4 || ldb < (int64_t)N) ? 0 : skn_plan(M, N, K).split;
         if (M > 64) return 0;
     } else if (ab_type != VKB_T_F16 && ab_type != VKB_T_BF16) {
         return 0;
