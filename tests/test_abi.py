@@ -167,8 +167,10 @@ def test_plan_headline_configs():
         for dt in (vk.DT_F16, vk.DT_BF16):
             pl = P(dt, dt, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192)
             assert pl.path == vk.PATH_SKINNY
-    # 25-64 tokens at 8192^2: the short-M pipelined tiles with a K split
-    assert P(vk.DT_F16, vk.DT_F16, 0, 1, 64, 8192, 8192, 8192, 8192, 8192).path == vk.PATH_SPLITK
+    # up to 64 tokens at 8192^2: the decode kernels (weights above 12288 x
+    # 4096 elements keep them for 33-64 rows too)
+    for ntok in (32, 48, 64):
+        assert P(vk.DT_F16, vk.DT_F16, 0, 1, ntok, 8192, 8192, 8192, 8192, 8192).path == vk.PATH_SKINNY
     # 65 tokens: a GEMM again
     assert P(vk.DT_F16, vk.DT_F16, 0, 1, 65, 8192, 8192, 8192, 8192, 8192).path != vk.PATH_SKINNY
     # not skinny when misaligned or batched
@@ -247,13 +249,14 @@ def test_plan_decode_split():
         assert split(M, 14336, 4096) == 2     # 112 per slice: 224 workgroups
         assert split(M, 4096, 14336) == 8     # 32 per slice
     assert split(32, 4096, 14336) == 8
-    # 25-64 rows (33-64 against N < 8192): the decode kernels where the
-    # short-M tiles do not apply (K below 4096, more than 128 column tiles)
+    # 33-64 rows: the decode kernels where the short-M tiles do not apply (K
+    # below 4096, more than 128 column tiles, a weight above 12288 x 4096)
     assert split(64, 8192, 2048) == 4 and split(48, 40000, 8192) == 1
+    assert split(64, 8192, 8192) == 4 and split(40, 14336, 4096) == 2 and split(64, 4096, 14336) == 8
     # and otherwise the short-M pipelined tiles with a K split
-    for M, N in ((25, 8192), (64, 8192), (33, 4096)):
-        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, M, N, 8192, 8192, 8192, N)
-        assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 1) and pl.split >= 2
+    for M, N, K in ((33, 4096, 8192), (64, 4096, 4096), (40, 11008, 4096), (64, 12288, 4096)):
+        pl = P(vk.DT_F16, vk.DT_F16, 0, 1, M, N, K, K, K, N)
+        assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 1) and pl.split >= 2, (M, N, K)
     assert split(32, 256, 8192) == 16         # 2 per slice, 64 steps: 4 per slice
     assert split(32, 256, 1024) == 2          # 8 steps: at least 4 per slice
     assert split(32, 40000, 8192) == 1        # more than one round already

@@ -362,17 +362,21 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
      * 1.6-2.2x slower (edge rows).  vkb_skinny_plan holds the
      * kernels' own limits (leading dimensions, 32-bit buffer spans) and
      * returns their K split, or 0: then a tile path. */
-    /* 16-bit, 33-64 rows (25-64 against N >= 8192), K >= 4096 and at most
-     * 128 column tiles of 128: the short-M pipelined tiles with a K split
-     * (below) beat the decode kernels.  fp16, one box: N = 14336 / 11008 /
-     * 4096, K = 4096, M = 64 34.6 / 32.6 / 17.7 -> 26.4 / 22.4 / 14.3 us,
-     * M = 40 29.7 / 27.0 / 13.7 -> 25.1 / 21.3 / 12.4, M = 24 24.6 / 22.1 /
-     * 11.6 -> 24.0 / 20.9 / 11.8; 8192^2 M = 64 32.5 -> 27.9 (weight K x N
-     * 35.4 -> 29.1), M = 24 27.8 -> 25.3.  With more column tiles (N =
-     * 28672, unsplit tiles) the decode kernels stay ahead (92.6 against
-     * 108.1 us at 64 rows). */
-    const int tiles_first = ab_type != VKBLAS_DT_F32 && M > (N >= 8192 ? 24u : 32u) && K >= 4096 && split_k == 0 &&
-                            batch == 1 &&
+    /* 16-bit, 33-64 rows against a weight of at most 12288 x 4096 elements,
+     * K >= 4096 and at most 128 column tiles of 128: the short-M pipelined
+     * tiles with a K split (below) beat the decode kernels.  fp16, one box,
+     * three weight copies rotated per call (no reuse of the 256 MB MALL
+     * between calls), M = 40 / 48 / 64, decode -> tiles: 4096^2 15.3 / 15.7 /
+     * 18.6 -> 13.5 / 13.4 / 14.4 us, 11008 x 4096 27.6 / 29.4 / 32.8 -> 22.7 /
+     * 23.2 / 24.8, 12288 x 4096 28.6 / 30.5 / 33.7 -> 27.0 / 27.6 / 28.5.
+     * Larger weights keep the decode kernels: 8192^2 29.9 / 30.5 / 32.8
+     * against 39.4 / 39.6 / 40.4 on tiles (weight K x N 32.1 / 32.0 / 35.2
+     * against 33.6 / 35.9 / 37.9), 14336 x 4096 29.9 / 31.5 / 34.3 against
+     * 34.1 / 34.4 / 35.0, 4096 x 14336 27.2 / 28.0 / 31.8 against 29.7 /
+     * 29.0 / 29.3.  (With one weight resident in MALL the tiles measure
+     * 25-28 us at 8192^2: a single-weight loop overstates them.) */
+    const int tiles_first = ab_type != VKBLAS_DT_F32 && M > 32u && (uint64_t)N * K <= 12288ull * 4096ull &&
+                            K >= 4096 && split_k == 0 && batch == 1 &&
                             g_force_tile < 0 && cdiv(N, 128) <= 128 &&
                             pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned);
     if (op_a == VKBLAS_OP_N && batch == 1 && split_k <= 1 && aligned && !g_no_skinny && !tiles_first &&
