@@ -447,6 +447,7 @@ def main():
     line["fp16_matvec_8192_KxO"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8, 16, 32), kxo=True)
     log("[bench] fp32 matvec 8192x8192, both weight layouts")
     line["fp32_matvec_8192"] = matvec_f32(torch, vk, stream, args.steps)
+    line["fp32_decode_8192_wide"] = matvec_f32(torch, vk, stream, args.steps, ntoks=(32, 64))
     log("[bench] split-K and strided-batched")
     line["splitk_256x256"] = splitk(torch, vk, stream, args.steps)
     line["batched_fp32_64x512"] = batched(torch, vk, stream, args.steps)
