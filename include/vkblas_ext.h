@@ -17,6 +17,14 @@ extern "C" {
 
 typedef enum { VKBLAS_DT_F32 = 0, VKBLAS_DT_F16 = 1, VKBLAS_DT_BF16 = 2 } vkblas_dtype_t;
 
+/* Status of the stream-aware entry points (beyond vkblas_status_t): a
+ * kernel launch failed after an earlier kernel of the same call had been
+ * enqueued to write part of C.  C may then hold results for some rows, so
+ * the call must not be repeated by another library on the same C: the
+ * hipBLAS, rocBLAS and hipBLASLt entry points report an execution failure
+ * for it instead of forwarding the call to the vendor library. */
+#define VKBLAS_ERR_PARTIAL ((vkblas_status_t)5)
+
 /* How alpha / beta are passed (hipBLAS pointer modes). */
 typedef enum {
     VKBLAS_SCALAR_HOST = 0,     /* the float alpha / beta arguments          */
@@ -68,7 +76,9 @@ typedef struct {
  *   split_k: 0 = heuristic, 1 = never split, >1 = force that many K slices
  *            (clamped so every slice is non-empty).
  * Returns VKBLAS_OK, VKBLAS_ERR_PARAM (bad arguments / unsupported type
- * combination) or VKBLAS_ERR_INIT (no GPU, launch failure).  Asynchronous:
+ * combination), VKBLAS_ERR_INIT (no GPU, launch failure before anything
+ * was enqueued to write C) or VKBLAS_ERR_PARTIAL (a launch failed after part
+ * of C was enqueued to be written: the split tail).  Asynchronous:
  * C is valid once the stream reaches this point.
  */
 vkblas_status_t vkblas_gemm_async(

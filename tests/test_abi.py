@@ -448,3 +448,46 @@ def test_preload_env_keeps_existing_preloads():
     for bad in (["python3"], ["python3", "-u"], ["python3", "-c", "print(1)"]):
         with pytest.raises(ValueError):
             preload.torch_hipblas_command(bad)
+
+
+class _VkbEpi(ctypes.Structure):
+    # vkb_epilogue_args (vkblas_amd/csrc/vkb_launch.h)
+    _fields_ = [("c_in", ctypes.c_void_p), ("ldc_in", ctypes.c_int64), ("stride_c_in", ctypes.c_int64),
+                ("bias", ctypes.c_void_p), ("bias_type", ctypes.c_int)]
+
+
+class _VkbArgs(ctypes.Structure):
+    # vkb_gemm_args (vkblas_amd/csrc/vkb_launch.h)
+    _fields_ = [("A", ctypes.c_void_p), ("B", ctypes.c_void_p), ("C", ctypes.c_void_p),
+                ("lda", ctypes.c_int64), ("ldb", ctypes.c_int64), ("ldc", ctypes.c_int64),
+                ("stride_a", ctypes.c_int64), ("stride_b", ctypes.c_int64), ("stride_c", ctypes.c_int64),
+                ("M", ctypes.c_uint32), ("N", ctypes.c_uint32), ("K", ctypes.c_uint32), ("batch", ctypes.c_uint32),
+                ("split", ctypes.c_uint32), ("k_per_split", ctypes.c_uint32), ("stride_split", ctypes.c_int64),
+                ("a_kmajor", ctypes.c_int), ("b_kmajor", ctypes.c_int), ("ab_type", ctypes.c_int),
+                ("c_type", ctypes.c_int), ("alpha", ctypes.c_float), ("beta", ctypes.c_float),
+                ("scalar_mode", ctypes.c_int), ("alpha_dev", ctypes.c_void_p), ("beta_dev", ctypes.c_void_p),
+                ("generic_only", ctypes.c_int), ("ptr_array", ctypes.c_int),
+                ("kernel_out", ctypes.POINTER(ctypes.c_int)), ("epi", ctypes.POINTER(_VkbEpi))]
+
+
+@pytest.mark.parametrize("dt", [0, 1, 2])
+def test_launcher_rejects_pointer_array_with_separate_c(dt):
+    """The tile launcher refuses a pointer-array batch with a separate C
+    input (no per-batch C_in pointers exist) and a pointer-array split, and
+    decides it from the arguments alone: both return hipErrorInvalidValue (1)
+    before any device call, so this runs without a GPU.  A regression test of
+    the launcher reading its parameter block's pointer-array flag before
+    setting it."""
+    eng = ctypes.CDLL(vk.ENGINE_PATH)
+    fn = eng.vkb_launch_gemm
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(_VkbArgs), ctypes.c_int, ctypes.c_void_p]
+    epi = _VkbEpi(c_in=0x10000, ldc_in=256, stride_c_in=0, bias=None, bias_type=0)
+    a = _VkbArgs(A=0x1000, B=0x2000, C=0x3000, lda=256, ldb=256, ldc=256, M=256, N=256, K=256, batch=4,
+                 split=1, k_per_split=256, a_kmajor=1, b_kmajor=1, ab_type=dt, c_type=dt, alpha=1.0, beta=1.0,
+                 ptr_array=1, epi=ctypes.pointer(epi))
+    for tile in (0, 1, 2):
+        assert fn(ctypes.byref(a), tile, None) == 1
+    a.epi = None
+    a.split, a.k_per_split, a.stride_split = 2, 128, 65536
+    assert fn(ctypes.byref(a), 1, None) == 1

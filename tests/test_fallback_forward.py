@@ -207,3 +207,30 @@ def test_rocblas_engine_failure_forwards(layer):
         assert c.fn == b"rocblas_gemm_ex" and (c.m, c.n, c.k, c.ldc) == (64, 32, 128, 64)
         assert (c.alpha, c.beta) == (1.5, -0.25)
     """)
+
+
+def test_partial_write_failure_is_reported_not_forwarded(layer):
+    """VKBLAS_ERR_PARTIAL (5): a launch failed after a kernel writing part of
+    C was enqueued (the split tail's head tiles).  Forwarding would let the
+    vendor read those rows as its input C, so hipBLAS reports
+    HIPBLAS_STATUS_EXECUTION_FAILED (5) and the vendor is not called."""
+    run_case(layer, """
+        st = L.hipblasSgemm(h, N, N, 40, 24, 16, ctypes.byref(alpha), A, 40, B, 16, ctypes.byref(beta), C, 40)
+        assert st == 5, st
+        assert eng.fake_engine_calls() == 1
+        assert last(hb).calls == 0
+    """, status=5)
+
+
+def test_rocblas_partial_write_failure_is_reported_not_forwarded(layer):
+    """The rocBLAS layer reports rocblas_status_internal_error (6) for it."""
+    run_case(layer, """
+        f16, f32 = 150, 151
+        rh = ctypes.c_void_p()
+        assert rb.rocblas_create_handle(ctypes.byref(rh)) == 0
+        st = L.rocblas_gemm_ex(rh, T, N, 64, 32, 128, ctypes.byref(alpha), A, f16, 128, B, f16, 128,
+                               ctypes.byref(beta), C, f16, 64, C, f16, 64, f32, 0, 0, 0)
+        assert st == 6, st
+        assert eng.fake_engine_calls() == 1
+        assert last(rb).calls == 0
+    """, status=5)

@@ -148,6 +148,15 @@ def test_separate_d_and_device_scalars(rh):
     dA, dB, dC = to_dev(A), to_dev(B), to_dev(C)
     dD = torch.full((m * n,), float("nan"), dtype=torch.float16, device="cuda:0")
     scal = torch.tensor([2.0, 0.5], dtype=torch.float32, device="cuda:0")
+    # a decode call first: a call the engine computes replaces its path as
+    # vkblas_last_path, a forwarded one leaves it
+    import vkblas_amd as vk
+    x = torch.zeros(2 * 64, dtype=torch.float16, device="cuda:0")
+    w = torch.zeros(64 * 64, dtype=torch.float16, device="cuda:0")
+    vk.gemm_async(vk.DT_F16, vk.DT_F16, 0, 1, 2, 64, 64, 1.0, x.data_ptr(), 64, w.data_ptr(), 64, 0.0,
+                  x.data_ptr(), 64)
+    torch.cuda.synchronize()
+    assert vk.last_path() == vk.PATH_SKINNY
     rh.set_pointer_mode(DEVICE)
     try:
         st = rh.lib.rocblas_gemm_ex(rh.h, OP[0], OP[0], m, n, k, scal.data_ptr(), dA.data_ptr(), F16, m,
@@ -156,6 +165,7 @@ def test_separate_d_and_device_scalars(rh):
     finally:
         rh.set_pointer_mode(HOST)
     assert st == 0
+    assert vk.last_path() != vk.PATH_SKINNY, "the call was forwarded"
     assert normwise(oracle.h2f(to_host(dD)), oracle.h2f(want)) <= F16_BOUND
     assert np.array_equal(to_host(dC), C)   # C is read-only
 

@@ -648,6 +648,7 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
     const int ct = kernel_type(c_type);
     const hipStream_t hs = (hipStream_t)stream;
     int rc = 0;
+    int c_written = 0; /* a kernel writing part of C was enqueued before a later launch of this call failed */
     int kernel = VKBLAS_KERNEL_SKINNY;
     if (g_trace)
         fprintf(stderr, "[vkblas] gemm %s%s %s->%s M=%u N=%u K=%u lda=%u ldb=%u ldc=%u batch=%u path=%s split=%u%s\n",
@@ -729,11 +730,14 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
         a.epi = epp;
         if (plan.path == VKBLAS_PATH_TAIL) {
             /* rows [0, head) as tiles, rows [head, M) split-K into the
-             * workspace and reduced into C with the epilogue; batch == 1 */
+             * workspace and reduced into C with the epilogue; batch == 1.
+             * The tail's pass 1 goes first: it writes only the workspace, so
+             * a failure there or at the head's launch leaves C untouched and
+             * the caller may forward the call; a failure after the head's
+             * tiles were enqueued returns VKBLAS_ERR_PARTIAL. */
             const uint32_t head = M - plan.tail_rows;
             const size_t es_ab = ab == VKB_T_F32 ? 4 : 2, es_c = ct == VKB_T_F32 ? 4 : 2;
             a.M = head;
-            rc = vkb_launch_gemm(&a, plan.tile, stream);
             vkb_gemm_args t = a;
             t.M = plan.tail_rows;
             t.A = (const char*)A + (size_t)head * (op_a == VKBLAS_OP_N ? (size_t)lda : 1) * es_ab;
@@ -749,7 +753,9 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
             t.epi = NULL;
             int tail_kernel = 0;
             t.kernel_out = &tail_kernel;
-            if (rc == 0) rc = vkb_launch_gemm(&t, plan.tile, stream);
+            rc = vkb_launch_gemm(&t, plan.tile, stream);
+            if (rc == 0) rc = vkb_launch_gemm(&a, plan.tile, stream);
+            if (rc == 0) c_written = 1;
             vkb_epilogue_args tep;
             memset(&tep, 0, sizeof(tep));
             if (epp) {
@@ -784,8 +790,9 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
     ws_release(&lease);
     prof_end(&pf, hs, path_name(plan.path), rc == 0);
     if (rc != 0) {
-        if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s\n", hipGetErrorString((hipError_t)rc));
-        return VKBLAS_ERR_INIT;
+        if (g_trace) fprintf(stderr, "[vkblas] launch failed: %s%s\n", hipGetErrorString((hipError_t)rc),
+                             c_written ? " (after part of C was written)" : "");
+        return c_written ? VKBLAS_ERR_PARTIAL : VKBLAS_ERR_INIT;
     }
     g_last_path = plan.path;
     g_last_kernel = kernel;

@@ -59,7 +59,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     else if (tile == VKB_TILE_256) { bm = bn = 256; }
     else if (tile != VKB_TILE_64) return (int)hipErrorInvalidValue;
 
-    KParams p;
+    KParams p{};
     p.A = a->A; p.B = a->B; p.C = a->C;
     p.lda = a->lda; p.ldb = a->ldb; p.ldc = a->ldc;
     p.sa = a->stride_a; p.sb = a->stride_b; p.sc = a->stride_c;
@@ -80,9 +80,9 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     p.epi.scin = sep_cin ? ep->stride_c_in : a->stride_c;
     p.epi.bias = (ep && p.split == 1) ? ep->bias : nullptr;
     p.epi.bias_type = ep ? ep->bias_type : 0;
+    p.ptr_array = a->ptr_array != 0;
     if (p.ptr_array && sep_cin) return (int)hipErrorInvalidValue;   // Cin pointers are not given
     const bool multi = p.batch > 1;
-    p.ptr_array = a->ptr_array != 0;
     if (p.ptr_array) {
         // the matrices' alignment is checked per batch in the kernel, which
         // always runs the checked instantiation (no pipelined kernel)

@@ -245,6 +245,12 @@ static hipblasStatus_t run_gemm_any(hipblasHandle_t handle, vkblas_dtype_t ab, v
         st = vkblas_gemm_async(ab, ct, op_a, op_b, (uint32_t)n, (uint32_t)m, (uint32_t)k, a, B, (uint32_t)ldb, A,
                                (uint32_t)lda, b, C, (uint32_t)ldc, (uint32_t)batch, batch > 1 ? sB : 0,
                                batch > 1 ? sA : 0, batch > 1 ? sC : 0, sm, ad, bd, 0, stream);
+    if (st == VKBLAS_ERR_PARTIAL) {
+        /* part of C may already be written: repeating the call elsewhere
+         * could read it as its input C */
+        if (g_trace) fprintf(stderr, "[vkblas] engine status %d: execution failed, not forwarded\n", (int)st);
+        return HIPBLAS_STATUS_EXECUTION_FAILED;
+    }
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return VKB_DECLINE;

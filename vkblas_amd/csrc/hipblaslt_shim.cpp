@@ -282,7 +282,10 @@ bool decline(const char* why) {
 
 bool run(hipblasLtMatmulDesc_t desc, const void* alpha, const void* A, hipblasLtMatrixLayout_t Adesc,
          const void* B, hipblasLtMatrixLayout_t Bdesc, const void* beta, const void* C,
-         hipblasLtMatrixLayout_t Cdesc, void* D, hipblasLtMatrixLayout_t Ddesc, hipStream_t stream) {
+         hipblasLtMatrixLayout_t Cdesc, void* D, hipblasLtMatrixLayout_t Ddesc, hipStream_t stream,
+         bool* failed) {
+    // *failed: the engine failed after part of D was written (not forwarded)
+    *failed = false;
     pthread_once(&g_once, real_open);
     if (!desc || !alpha || !beta || !A || !B || !D) return decline("null argument");
     DescRec dr;
@@ -370,6 +373,11 @@ bool run(hipblasLtMatmulDesc_t desc, const void* alpha, const void* A, hipblasLt
         at, dt, op_a, op_b, (uint32_t)n, (uint32_t)m, (uint32_t)k, a, B, (uint32_t)lb.ld, A, (uint32_t)la.ld, b, D,
         (uint32_t)ld.ld, (uint32_t)batch, batch > 1 ? lb.stride : 0, batch > 1 ? la.stride : 0,
         batch > 1 ? ld.stride : 0, sm, ad, bd, 0, (epi.bias || epi.c_in) ? &epi : nullptr, (void*)stream);
+    if (st == VKBLAS_ERR_PARTIAL) {
+        if (g_trace) fprintf(stderr, "[vkblas] engine status %d: execution failed, not forwarded\n", (int)st);
+        *failed = true;
+        return false;
+    }
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return false;
@@ -465,8 +473,10 @@ hipblasStatus_t hipblasLtMatmul(hipblasLtHandle_t handle, hipblasLtMatmulDesc_t 
                                 hipblasLtMatrixLayout_t Cdesc, void* D, hipblasLtMatrixLayout_t Ddesc,
                                 const hipblasLtMatmulAlgo_t* algo, void* workspace, size_t workspaceSizeInBytes,
                                 hipStream_t stream) {
-    if (handle && run(matmulDesc, alpha, A, Adesc, B, Bdesc, beta, C, Cdesc, D, Ddesc, stream))
+    bool failed = false;
+    if (handle && run(matmulDesc, alpha, A, Adesc, B, Bdesc, beta, C, Cdesc, D, Ddesc, stream, &failed))
         return HIPBLAS_STATUS_SUCCESS;
+    if (failed) return HIPBLAS_STATUS_EXECUTION_FAILED;
     typedef hipblasStatus_t (*fn_t)(hipblasLtHandle_t, hipblasLtMatmulDesc_t, const void*, const void*,
                                     hipblasLtMatrixLayout_t, const void*, hipblasLtMatrixLayout_t, const void*,
                                     const void*, hipblasLtMatrixLayout_t, void*, hipblasLtMatrixLayout_t,

@@ -135,7 +135,8 @@ static int dtype_of(rocblas_datatype t, vkblas_dtype_t* out) {
     return 0;
 }
 
-/* 0 = computed; 1 = declined (the caller forwards). */
+/* 0 = computed; 1 = declined (the caller forwards); 2 = failed after part
+ * of D was written (the caller reports it and does not forward). */
 static int run(const gemm_call* g) {
     pthread_once(&g_once, real_open);
     if (!g->handle || !g->alpha || !g->beta || !g->a || !g->b || !g->d) return 1;
@@ -213,6 +214,10 @@ static int run(const gemm_call* g) {
                                   (uint32_t)g->ldb, g->a, (uint32_t)g->lda, beta, g->d, (uint32_t)g->ldd,
                                   (uint32_t)g->batch, g->batch > 1 ? g->sb : 0, g->batch > 1 ? g->sa : 0,
                                   g->batch > 1 ? g->sd : 0, sm, ad, bd, 0, epi.c_in ? &epi : NULL, stream);
+    if (st == VKBLAS_ERR_PARTIAL) {
+        if (g_trace) fprintf(stderr, "[vkblas] engine status %d: execution failed, not forwarded\n", (int)st);
+        return 2;
+    }
     if (st != VKBLAS_OK) {
         if (g_trace) fprintf(stderr, "[vkblas] engine status %d: forwarding\n", (int)st);
         return 1;
@@ -254,7 +259,9 @@ rocblas_status(rocblas_gemm_ex)(rocblas_handle handle, rocblas_operation transA,
                                 uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
                          c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags, 0};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_ex_t f = (gemm_ex_t)cached_sym(&fn, "rocblas_gemm_ex");
     if (!f) return rocblas_status_not_implemented;
@@ -271,7 +278,9 @@ rocblas_status(rocblas_gemm_ex_64)(rocblas_handle handle, rocblas_operation tran
                                    uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
                          c, c_type, ldc, 0, d, d_type, ldd, 0, 1, compute_type, flags, 0};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_ex64_t f = (gemm_ex64_t)cached_sym(&fn, "rocblas_gemm_ex_64");
     if (!f) return rocblas_status_not_implemented;
@@ -289,7 +298,9 @@ rocblas_status(rocblas_gemm_strided_batched_ex)(
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, stride_a, b, b_type, ldb,
                          stride_b, beta, c, c_type, ldc, stride_c, d, d_type, ldd, stride_d, batch_count,
                          compute_type, flags, 0};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_sb_t f = (gemm_sb_t)cached_sym(&fn, "rocblas_gemm_strided_batched_ex");
     if (!f) return rocblas_status_not_implemented;
@@ -308,7 +319,9 @@ rocblas_status(rocblas_gemm_strided_batched_ex_64)(
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, stride_a, b, b_type, ldb,
                          stride_b, beta, c, c_type, ldc, stride_c, d, d_type, ldd, stride_d, batch_count,
                          compute_type, flags, 0};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_sb64_t f = (gemm_sb64_t)cached_sym(&fn, "rocblas_gemm_strided_batched_ex_64");
     if (!f) return rocblas_status_not_implemented;
@@ -340,7 +353,9 @@ rocblas_status(rocblas_gemm_batched_ex)(rocblas_handle handle, rocblas_operation
                                         rocblas_gemm_algo algo, int32_t solution_index, uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
                          c, c_type, ldc, 0, d, d_type, ldd, 0, batch_count, compute_type, flags, 1};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_b_t f = (gemm_b_t)cached_sym(&fn, "rocblas_gemm_batched_ex");
     if (!f) return rocblas_status_not_implemented;
@@ -358,7 +373,9 @@ rocblas_status(rocblas_gemm_batched_ex_64)(rocblas_handle handle, rocblas_operat
                                            int32_t solution_index, uint32_t flags) {
     const gemm_call g = {handle, transA, transB, m, n, k, alpha, a, a_type, lda, 0, b, b_type, ldb, 0, beta,
                          c, c_type, ldc, 0, d, d_type, ldd, 0, batch_count, compute_type, flags, 1};
-    if (run(&g) == 0) return rocblas_status_success;
+    const int r = run(&g);
+    if (r == 0) return rocblas_status_success;
+    if (r == 2) return rocblas_status_internal_error;
     static void* fn;
     gemm_b64_t f = (gemm_b64_t)cached_sym(&fn, "rocblas_gemm_batched_ex_64");
     if (!f) return rocblas_status_not_implemented;

@@ -1224,7 +1224,7 @@ extern "C" int vkb_launch_skinny(int ab_type, int b_kmajor, const void* X, int64
     if (want == 0 || nsplit != want || (nsplit > 1 && !part)) return (int)hipErrorInvalidValue;
     if (c_type != VKB_T_F32 && c_type != ab_type) return (int)hipErrorInvalidValue;
     if (((uintptr_t)X & 15) || ((uintptr_t)W & 15)) return (int)hipErrorInvalidValue;
-    SkParams p;
+    SkParams p{};
     p.X = X; p.W = W; p.C = C;
     p.lda = lda; p.ldb = ldb; p.ldc = ldc;
     p.M = M; p.N = N; p.K = K;
