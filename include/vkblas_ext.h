@@ -53,12 +53,15 @@ typedef enum {
     VKBLAS_KERNEL_PIPE256 = 3,          /* pipelined kernel, 256 x 256 tiles       */
     VKBLAS_KERNEL_PIPE128 = 4,          /* pipelined kernel, 128 x 128, 2 stages   */
     VKBLAS_KERNEL_PIPE128_4 = 5,        /* pipelined kernel, 128 x 128, 4 stages   */
-    VKBLAS_KERNEL_SKINNY = 6            /* decode kernels                          */
+    VKBLAS_KERNEL_SKINNY = 6,           /* decode kernels                          */
+    VKBLAS_KERNEL_WAVEK = 7             /* split-K pass 1 on 32 x 32 / 64 x 64
+                                           tiles, the slice's K over the waves  */
 } vkblas_kernel_t;
 
 typedef struct {
     int path;              /* vkblas_path_t                                 */
-    int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256)  */
+    int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256,
+                              3:32 for split-K pass 1)                     */
     uint32_t split;        /* split-K factor, 1 = no split (VKBLAS_PATH_TAIL:
                               the split of the tail rows)                  */
     uint32_t k_per_split;  /* K per split (multiple of the tile's K step)   */

@@ -393,8 +393,9 @@ def test_plan_forced_split(K, split, dt):
     assert pl.split * pl.k_per_split >= K > (pl.split - 1) * pl.k_per_split
     assert pl.split == split
     # 64 slices of the four 128x128 tiles fill the CUs: the pipelined
-    # 128x128 kernel; fewer slices keep the 64x64 tiles
-    assert pl.tile == (1 if split == 64 else 0)
+    # 128x128 kernel; 16 slices of 64x64 tiles or 4 of 32x32 (tile code 3)
+    # do on the wave-K kernel
+    assert pl.tile == {64: 1, 16: 0, 4: 3}[split]
 
 
 def test_plan_split_heuristic_and_off():
@@ -491,3 +492,41 @@ def test_launcher_rejects_pointer_array_with_separate_c(dt):
     a.epi = None
     a.split, a.k_per_split, a.stride_split = 2, 128, 65536
     assert fn(ctypes.byref(a), 1, None) == 1
+
+
+def test_plan_caller_split_small_tiles():
+    """A caller's split whose 128x128 tiles give fewer than 224 workgroups:
+    split-K pass 1 on 64x64 tiles (the wave-K kernel) when they give at least
+    224, else on 32x32 tiles (tile code 3); M = N = 256 at BASELINE
+    configs[4]'s splits 4 / 16 / 64."""
+    for dt in (vk.DT_F32, vk.DT_F16, vk.DT_BF16):
+        for K in (65536, 262144):
+            for split, tile in ((4, 3), (16, 0), (64, 1)):
+                pl = P(dt, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256, split_k=split)
+                assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, split, tile), (dt, K, split, pl.tile)
+    # ragged for 64x64 but whole 32x32 tiles: 32x32
+    pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 192, 96, 4096, 4096, 96, 96, split_k=5)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 3)
+    # not whole 32x32 tiles: the generic kernel's 64x64 tiles
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 200, 96, 4096, 4096, 96, 96, split_k=5)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
+    # K not in whole 64-k steps: no wave-K plan for 16-bit inputs (fp32 steps are 32 k)
+    pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 8288, 8288, 256, 256, split_k=4)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 8288, 8288, 256, 256, split_k=4)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 3)
+    # unaligned operands: no wave-K plan either
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 8192, 8192, 256, 256, split_k=4, aligned=False)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
+
+
+def test_plan_caller_split_collapsing_to_one_slice():
+    """A split over a K within one slice runs a tile plan, never 32x32."""
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 32, 32, 256, 256, split_k=4)
+    assert pl.split == 1 and pl.tile in (0, 1, 2)
+    vk.set_override(-1, True)
+    try:
+        pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=4)
+        assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
+    finally:
+        vk.set_override(-1, False)

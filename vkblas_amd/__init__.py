@@ -132,7 +132,7 @@ def last_path() -> int:
 
 # vkblas_kernel_t (include/vkblas_ext.h)
 KERNEL_NONE, KERNEL_GENERIC, KERNEL_GENERIC_CHECKED, KERNEL_PIPE256, KERNEL_PIPE128, KERNEL_PIPE128_4, \
-    KERNEL_SKINNY = range(7)
+    KERNEL_SKINNY, KERNEL_WAVEK = range(8)
 
 
 def workspace_release() -> None:

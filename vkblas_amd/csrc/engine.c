@@ -320,6 +320,21 @@ static int pipe_ok(vkblas_dtype_t ab_type, int tile, vkblas_op_t op_a, vkblas_op
            lda % vec == 0 && ldb % vec == 0;
 }
 
+/* Split-K pass 1 on tt x tt tiles (32 or 64) by the wave-K kernel (its
+ * launcher's conditions): whole tiles, K in whole steps (32 k for fp32, 64
+ * for 16-bit types; the planner's slices are multiples of that), aligned
+ * operands and leading dimensions, operand spans below 2^31 bytes. */
+static int wavek_ok(vkblas_dtype_t ab_type, uint32_t tt, vkblas_op_t op_a, vkblas_op_t op_b, uint32_t M, uint32_t N,
+                    uint32_t K, uint32_t lda, uint32_t ldb, int aligned) {
+    const uint32_t vec = ab_type == VKBLAS_DT_F32 ? 4 : 8;
+    const uint64_t es = ab_type == VKBLAS_DT_F32 ? 4 : 2;
+    const uint64_t span_a = ((uint64_t)(op_a == VKBLAS_OP_N ? tt : K) * lda + K) * es;
+    const uint64_t span_b = ((uint64_t)(op_b == VKBLAS_OP_T ? tt : K) * ldb + K) * es;
+    return aligned && !g_generic_only && M % tt == 0 && N % tt == 0 && K % (vec == 4 ? 32 : 64) == 0 &&
+           lda % vec == 0 &&
+           ldb % vec == 0 && span_a < (1ull << 31) && span_b < (1ull << 31);
+}
+
 /* Tile choice for 256 CUs: the largest tile that still gives about one
  * workgroup per CU; smaller tiles only when the large one would starve. */
 static int choose_tile(uint32_t M, uint32_t N, uint32_t batch) {
@@ -425,6 +440,14 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             if (g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
                 (uint64_t)cdiv(M, 128) * cdiv(N, 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
                 tile = VKB_TILE_128;
+            /* fewer: the wave-K kernel on 64x64 tiles if they give at least
+             * 224 workgroups, else on 32x32 tiles (M = N = 256: split 16 ->
+             * 256 workgroups of 64x64, split 4 -> 256 of 32x32) */
+            else if (g_force_tile < 0 && wavek_ok(ab_type, 64, op_a, op_b, M, N, K, lda, ldb, aligned) &&
+                     (uint64_t)(M / 64) * (N / 64) * split_k >= 224)
+                tile = VKB_TILE_64;
+            else if (g_force_tile < 0 && wavek_ok(ab_type, 32, op_a, op_b, M, N, K, lda, ldb, aligned))
+                tile = VKB_TILE_32;
         } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
                    (uint64_t)cdiv(M, 128) * cdiv(N, 128) <= 128 && K >= 4096) {
             /* 128x128 tiles, at most 128 of them (at most half the CUs), and
@@ -508,6 +531,9 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             plan->k_per_split = kps;
             return VKBLAS_OK;
         }
+        /* no split left (K within one slice): 32x32 tiles exist only for
+         * split-K pass 1 */
+        if (tile == VKB_TILE_32) tile = choose_tile(M, N, batch);
     }
     /* A partial last wave: with T tiles on `slots` concurrent workgroups
      * (one 256x256 or two 128x128 per CU on 256 CUs), T = W slots + R and

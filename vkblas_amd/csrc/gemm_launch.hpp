@@ -3,6 +3,7 @@
 #pragma once
 #include "gemm_mfma.hpp"
 #include "gemm_pipe.hpp"
+#include "gemm_wavek.hpp"
 #include "vkb_launch.h"
 
 namespace vkb {
@@ -50,6 +51,16 @@ static inline uint32_t cu_count() {
     return (uint32_t)n;
 }
 
+// Bytes of K per step of the wave-K kernel for 16-bit inputs: 128 (whole
+// 128-byte rows of a K-major operand per copy).  Measured against 64 (more
+// stages of half rows), M = N = 256, fp16, hipBLAS NN, split 4 / 16: K =
+// 65536 45.4 / 24.1 -> 36.7 / 19.8 us, K = 262144 163.5 / 83.1 -> 133.5 /
+// 66.5 us (two alternating runs, one box).
+#ifndef VKB_WAVEK_KB16
+#define VKB_WAVEK_KB16 128
+#endif
+constexpr int WK_KB16 = VKB_WAVEK_KB16;
+
 template <typename T, typename TC>
 static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     constexpr int VEC = Elem<T>::VEC;
@@ -57,6 +68,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     int bm = 64, bn = 64;
     if (tile == VKB_TILE_128) { bm = bn = 128; }
     else if (tile == VKB_TILE_256) { bm = bn = 256; }
+    else if (tile == VKB_TILE_32) { bm = bn = 32; }
     else if (tile != VKB_TILE_64) return (int)hipErrorInvalidValue;
 
     KParams p{};
@@ -178,6 +190,42 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             return (int)hipGetLastError();
         }
     }
+    // Split-K pass 1 on 32x32 or 64x64 tiles (few output tiles, a caller's
+    // split): the wave-K kernel, whose four waves each take a quarter of the
+    // slice's K.  Whole tiles, K and the slice in whole K steps, aligned
+    // operands; buffer offsets are signed 32-bit.
+    if constexpr (std::is_same<TC, float>::value) {
+        if ((tile == VKB_TILE_32 || tile == VKB_TILE_64) && p.split > 1 && !p.ptr_array && !a->generic_only) {
+            constexpr uint64_t ES = sizeof(T);
+            const uint32_t tt = (uint32_t)bm;
+            const uint64_t span_a = ((uint64_t)(ak ? tt : a->K) * (uint64_t)a->lda + a->K) * ES;
+            const uint64_t span_b = ((uint64_t)(bk ? tt : a->K) * (uint64_t)a->ldb + a->K) * ES;
+            constexpr uint32_t KS = sizeof(T) == 2 ? WK_KB16 / 2 : 32;   // k per step
+            if (a->M % tt == 0 && a->N % tt == 0 && a->K % KS == 0 && p.kps % KS == 0 && p.vec_a && p.vec_b &&
+                p.vec_c && span_a < (1ull << 31) && span_b < (1ull << 31)) {
+                report(VKB_KERN_WAVEK);
+                if (tt == 32) {
+                    if (ak) {
+                        if (bk) hipLaunchKernelGGL((gemm_wavek_kernel<T, true, true, 32, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_wavek_kernel<T, true, false, 32, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                    } else {
+                        if (bk) hipLaunchKernelGGL((gemm_wavek_kernel<T, false, true, 32, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_wavek_kernel<T, false, false, 32, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                    }
+                } else {
+                    if (ak) {
+                        if (bk) hipLaunchKernelGGL((gemm_wavek_kernel<T, true, true, 64, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_wavek_kernel<T, true, false, 64, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                    } else {
+                        if (bk) hipLaunchKernelGGL((gemm_wavek_kernel<T, false, true, 64, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                        else hipLaunchKernelGGL((gemm_wavek_kernel<T, false, false, 64, WK_KB16>), dim3(grid), dim3(256), 0, st, p);
+                    }
+                }
+                return (int)hipGetLastError();
+            }
+        }
+    }
+    if (tile == VKB_TILE_32) return (int)hipErrorInvalidValue;   // only the wave-K kernel takes 32x32 tiles
     report(full ? VKB_KERN_GENERIC : VKB_KERN_GENERIC_CHECKED);
     switch (tile) {
         case VKB_TILE_64:  return launch_layout<T, TC, VKB_TILE_64>(p, ak, bk, !full, grid, st);

@@ -132,7 +132,7 @@ extern "C" int vkb_launch_splitk_reduce(const float* P, int64_t stride_split, ui
 }
 
 extern "C" uint32_t vkb_tile_bm(int tile) {
-    return tile == VKB_TILE_256 ? 256u : tile == VKB_TILE_128 ? 128u : 64u;
+    return tile == VKB_TILE_256 ? 256u : tile == VKB_TILE_128 ? 128u : tile == VKB_TILE_32 ? 32u : 64u;
 }
 extern "C" uint32_t vkb_tile_bn(int tile) { return vkb_tile_bm(tile); }
 extern "C" uint32_t vkb_tile_bk(int ab_type) { return ab_type == VKB_T_F32 ? 32u : 64u; }

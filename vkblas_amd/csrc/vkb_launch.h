@@ -32,7 +32,9 @@ enum {
     VKB_KERN_PIPE256 = 3,          /* gemm_pipe_kernel, 256x256 tiles       */
     VKB_KERN_PIPE128 = 4,          /* gemm_pipe_kernel, 128x128, 2 stages   */
     VKB_KERN_PIPE128_4 = 5,        /* gemm_pipe_kernel, 128x128, 4 stages   */
-    VKB_KERN_SKINNY = 6            /* decode kernels (skinny.hip)           */
+    VKB_KERN_SKINNY = 6,           /* decode kernels (skinny.hip)           */
+    VKB_KERN_WAVEK = 7             /* gemm_wavek_kernel: split-K pass 1 on
+                                      32x32 / 64x64 tiles, K over the waves */
 };
 
 /* GEMM tile configurations (block tile BM x BN, 4 waves, BK = 128 bytes) */
@@ -40,7 +42,10 @@ enum {
     VKB_TILE_64  = 0,  /*  64 x  64, waves 2x2 of  32x32 */
     VKB_TILE_128 = 1,  /* 128 x 128, waves 2x2 of  64x64 */
     VKB_TILE_256 = 2,  /* 256 x 256, waves 2x2 of 128x128 */
-    VKB_TILE_COUNT = 3
+    VKB_TILE_COUNT = 3,
+    VKB_TILE_32 = 3    /* 32 x 32, split-K pass 1 only (gemm_wavek_kernel:
+                          each wave the whole tile over a quarter of the
+                          slice's K); not a choice for unsplit GEMMs */
 };
 
 /* Optional epilogue inputs (every launcher):
