@@ -18,7 +18,10 @@ The arithmetic lives in ``ref_gemm.c`` (built into ``liboracle.so`` by
 * ``f2bf_rne`` / ``bf2f`` -- bf16 conversions of
   ``src/shaders/gemm_half_128x128_bankfree_tmpl.comp:26-47``;
 * ``ref_gemm_bf16_rm`` -- ``src/vkblas.c:3345-3512`` (bf16 in, fp32
-  arithmetic, one bf16 rounding) on the row-major engine contract.
+  arithmetic, one bf16 rounding) on the row-major engine contract;
+* ``ref_gemm_tiled_rm`` -- the same arithmetic as ``ref_gemm_epi_rm`` in
+  cache-sized tiles, bit for bit equal to it, for whole-output checks of large
+  shapes.
 """
 from __future__ import annotations
 
@@ -81,6 +84,8 @@ def lib():
         _vp = ctypes.c_void_p
         L.oracle_ref_gemm_epi_rm.argtypes = [_int, _int, _int, _int, _int, _int, _int, _vp, _i64, _vp, _i64, _flt,
                                              _flt, _vp, _i64, _vp, _i64, _vp, rows_t, _int, _int]
+        L.oracle_ref_gemm_tiled_rm.argtypes = [_int, _int, _int, _int, _int, _int, _int, _vp, _i64, _vp, _i64,
+                                               _flt, _flt, _vp, _i64, _int]
         _lib = L
     return _lib
 
@@ -218,3 +223,11 @@ def ref_gemm_bf16f32_rm(op_a: int, op_b: int, M: int, N: int, K: int, A, lda: in
     p, n, keep = _rows_arg(rows)
     lib().oracle_ref_gemm_bf16f32_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc, p, n, threads)
     del keep
+
+
+def ref_gemm_tiled_rm(ab: str, ct: str, op_a: int, op_b: int, M: int, N: int, K: int, A, lda: int, B, ldb: int,
+                      alpha: float, beta: float, C, ldc: int, threads: int = 0) -> None:
+    """The whole output of ref_gemm_epi_rm (no bias, C_in == C), bit for bit, computed in cache-sized tiles:
+    for full-output checks of large shapes.  ab / ct: "f32", "f16" or "bf16"; in place on C (row-major)."""
+    lib().oracle_ref_gemm_tiled_rm(_TCODE[ab], _TCODE[ct], op_a, op_b, M, N, K, A.ctypes.data, lda, B.ctypes.data,
+                                   ldb, alpha, beta, C.ctypes.data, ldc, threads)

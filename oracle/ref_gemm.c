@@ -373,3 +373,68 @@ void oracle_ref_gemm_epi_rm(int ab, int ct, int op_a, int op_b, int M, int N, in
     }
     (void)threads;
 }
+
+/* --------------------------------------------- tiled, bit for bit the same */
+
+/* The arithmetic of oracle_ref_gemm_epi_rm (without bias, C_in == D) in an
+ * order that caches: operands are converted to double once (A as [k][m], B
+ * as [k][n]), and each thread keeps the double sums of a TM x TN block of C
+ * while k runs.  Every output is still the sum s = s + a_k b_k for k = 0 ..
+ * K-1 in that order, starting from 0 (the product of two floats is exact in
+ * double either way; the build contracts nothing into fused multiply-adds):
+ * the result equals the plain loops bit for bit (a test pins that).  For
+ * full-output checks of large shapes, which the plain loops take minutes
+ * over. */
+void oracle_ref_gemm_tiled_rm(int ab, int ct, int op_a, int op_b, int M, int N, int K, const void* A, int64_t lda,
+                              const void* B, int64_t ldb, float alpha, float beta, void* C, int64_t ldc,
+                              int threads) {
+    enum { TM = 64, TN = 256 };
+    h2f_lut_init();
+    double* Ad = (double*)malloc(sizeof(double) * (size_t)K * (size_t)M);
+    double* Bd = (double*)malloc(sizeof(double) * (size_t)K * (size_t)N);
+    if (!Ad || !Bd) {
+        free(Ad);
+        free(Bd);
+        abort();
+    }
+#ifdef _OPENMP
+    if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(threads)
+#endif
+    for (int k = 0; k < K; ++k) {
+        for (int m = 0; m < M; ++m)
+            Ad[(int64_t)k * M + m] = (double)load_t(ab, A, op_a ? (int64_t)k * lda + m : (int64_t)m * lda + k);
+        for (int n = 0; n < N; ++n)
+            Bd[(int64_t)k * N + n] = (double)load_t(ab, B, op_b ? (int64_t)n * ldb + k : (int64_t)k * ldb + n);
+    }
+    const int tm = (M + TM - 1) / TM, tn = (N + TN - 1) / TN;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+#endif
+    for (int t = 0; t < tm * tn; ++t) {
+        const int m0 = (t / tn) * TM, n0 = (t % tn) * TN;
+        const int mc = M - m0 < TM ? M - m0 : TM, nc = N - n0 < TN ? N - n0 : TN;
+        double* s = (double*)calloc((size_t)TM * TN, sizeof(double));
+        if (!s) abort();
+        for (int k = 0; k < K; ++k) {
+            const double* a = Ad + (int64_t)k * M + m0;
+            const double* b = Bd + (int64_t)k * N + n0;
+            for (int i = 0; i < mc; ++i) {
+                const double ai = a[i];
+                double* si = s + (int64_t)i * TN;
+#pragma omp simd
+                for (int j = 0; j < nc; ++j) si[j] += ai * b[j];
+            }
+        }
+        for (int i = 0; i < mc; ++i)
+            for (int j = 0; j < nc; ++j) {
+                const int64_t at = (int64_t)(m0 + i) * ldc + n0 + j;
+                const float old = beta != 0.0f ? load_t(ct, C, at) : 0.0f;
+                store_t(ct, C, at, alpha * (float)s[(int64_t)i * TN + j] + beta * old);
+            }
+        free(s);
+    }
+    free(Ad);
+    free(Bd);
+    (void)threads;
+}

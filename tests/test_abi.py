@@ -530,3 +530,47 @@ def test_plan_caller_split_collapsing_to_one_slice():
         assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
     finally:
         vk.set_override(-1, False)
+
+
+_KNOB_SCRIPT = r"""
+import sys
+sys.path.insert(0, {repo!r})
+import vkblas_amd as vk
+P = vk.plan
+out = []
+for dt in (vk.DT_F32, vk.DT_F16):
+    out.append(P(dt, vk.DT_F32, 0, 0, 4096, 4096, 4096, 4096, 4096, 4096).tile)
+    out.append(P(dt, vk.DT_F32, 0, 0, 2048, 2048, 2048, 2048, 2048, 2048).tile)
+    out.append(P(dt, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256).path)
+    out.append(P(dt, vk.DT_F32, 0, 0, 256, 256, 65536, 65536, 256, 256, split_k=4).path)
+print(out)
+"""
+
+
+@pytest.mark.parametrize("env,want", [
+    ({}, [2, 1, 4, 4, 2, 1, 4, 4]),
+    ({"VKBLAS_TILE128": "1"}, [1, 1, 4, 4, 1, 1, 4, 4]),
+    ({"VKBLAS_TILE128": "0"}, [0, 0, 4, 4, 0, 0, 4, 4]),
+    ({"VKBLAS_TILE128": "0", "VKBLAS_TILE": "256"}, [2, 2, 4, 4, 2, 2, 4, 4]),
+    ({"VKBLAS_NOSPLITK": "1"}, [2, 1, 1, 4, 2, 1, 1, 4]),
+    ({"VKBLAS_HSPLITK": "0"}, [2, 1, 4, 4, 2, 1, 1, 4]),
+    ({"VKBLAS_HT256": "0"}, [2, 1, 4, 4, 1, 1, 4, 4]),
+    ({"VKBLAS_HT256": "1"}, [2, 1, 4, 4, 2, 2, 4, 4]),
+])
+def test_reference_knob_names(env, want):
+    """The reference's path knobs under their own names (src/vkblas.c:915,
+    1356, 1637, 2858): per fp32 then fp16, the tile of 4096^3 and 2048^3,
+    the path at M = N = 256, K = 65536 planned and with a caller's split 4
+    (path 1 = 64x64 tiles, 4 = split-K).  Read once at load: one process
+    per setting."""
+    import json
+    import sys
+    e = dict(os.environ)
+    for k in ("VKBLAS_TILE", "VKBLAS_TILE128", "VKBLAS_NOSPLITK", "VKBLAS_HSPLITK", "VKBLAS_HT256",
+              "VKBLAS_SPLITK", "VKBLAS_KERNEL"):
+        e.pop(k, None)
+    e.update(env)
+    r = subprocess.run([sys.executable, "-c", _KNOB_SCRIPT.format(repo=REPO)], env=e, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    assert json.loads(r.stdout.strip().splitlines()[-1]) == want

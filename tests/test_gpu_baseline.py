@@ -143,6 +143,43 @@ def test_fp16_gemmex(handle, size, trans, out):
     assert normwise(g, r) <= F16_BOUND
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_full_output_4096(handle, dtype, ta, tb):
+    """configs 2 / 3 at 4096^3 with every element of C compared (the other
+    4096^3 cases sample 12 rows, as test_gemm.c:87 does): hipblasSgemm, or
+    hipblasGemmEx 16F x 16F -> 16F, in each layout, against the oracle in its
+    tiled form (bit for bit the plain oracle: tests/test_oracle.py)."""
+    from gpu_helpers import to_dev, to_host, fbox, normwise, f32_bound, F16_BOUND
+    from vkblas_amd import hipblas_abi as hb
+    n = 4096
+    f16 = dtype == "f16"
+    print(f"[case] full output {dtype} 4096^3 {'NT'[ta]}{'NT'[tb]}", flush=True)
+    if f16:
+        hA, hB = _fp16_inputs(70 + 2 * ta + tb, n * n, n), _fp16_inputs(80 + 2 * ta + tb, n * n, n)
+    else:
+        hA, hB = rng_uniform(90 + 2 * ta + tb, n * n), rng_uniform(100 + 2 * ta + tb, n * n)
+    dA, dB = to_dev(hA), to_dev(hB)
+    dC = torch.full((n * n,), float("nan"), dtype=torch.float16 if f16 else torch.float32, device="cuda:0")
+    ops = (hb.HIPBLAS_OP_N, hb.HIPBLAS_OP_T)
+    if f16:
+        st = handle.abi.hipblasGemmEx(handle.h, ops[ta], ops[tb], n, n, n, fbox(1.0), dA.data_ptr(), hb.HIP_R_16F,
+                                      n, dB.data_ptr(), hb.HIP_R_16F, n, fbox(0.0), dC.data_ptr(), hb.HIP_R_16F, n,
+                                      hb.HIPBLAS_COMPUTE_32F, hb.HIPBLAS_GEMM_DEFAULT)
+    else:
+        st = handle.abi.hipblasSgemm(handle.h, ops[ta], ops[tb], n, n, n, fbox(1.0), dA.data_ptr(), n,
+                                     dB.data_ptr(), n, fbox(0.0), dC.data_ptr(), n)
+    assert st == 0
+    got = to_host(dC)
+    # column-major C(m, n) is the engine's row-major C'(n, m) = op_b(B)' op_a(A)'
+    ref = np.zeros(n * n, np.uint16 if f16 else np.float32)
+    oracle.ref_gemm_tiled_rm(dtype, dtype, tb, ta, n, n, n, hB, n, hA, n, 1.0, 0.0, ref, n)
+    if f16:
+        got, ref = oracle.h2f(got), oracle.h2f(ref)
+    assert np.all(np.isfinite(got))
+    assert normwise(got, ref) <= (F16_BOUND if f16 else f32_bound(n))
+
+
 # ----------------------------------------------------------------- config 4
 
 MV = [(K, O, n) for (K, O) in [(8192, 8192), (4096, 14336), (14336, 4096)] for n in (1, 4, 8, 16)]
@@ -428,7 +465,7 @@ def test_strided_batched_64x512(handle):
     assert st == 0
     hGot = to_host(dC)
     rows = oracle.sample_rows(n, 12)
-    for b in (0, 1, 31, 63):
+    for b in range(nb):   # every batch, the same 12 sampled rows of each
         ref = np.zeros(s, np.float32)
         oracle.ref_gemm_cm(0, 0, n, n, n, 1.0, np.ascontiguousarray(hA[b * s:(b + 1) * s]), n,
                            np.ascontiguousarray(hB[b * s:(b + 1) * s]), n, 0.0, ref, n, 12, threads=0)

@@ -458,3 +458,29 @@ def test_ref_gemm_epi_planted_mistakes_fail():
     from_d = np.zeros(M * N, np.uint16)
     oracle.ref_gemm_epi_rm("f16", "f16", 0, 0, M, N, K, a, K, b, N, 1.0, 0.5, from_d, N, from_d, N, bias)
     assert not np.array_equal(D, from_d)
+
+
+@pytest.mark.parametrize("ab,ct", [("f32", "f32"), ("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"),
+                                   ("bf16", "f32"), ("f32", "f16")])
+@pytest.mark.parametrize("op_a,op_b", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_tiled_oracle_equals_plain_loops(ab, ct, op_a, op_b):
+    """ref_gemm_tiled_rm (whole-output checks of large shapes) is the plain
+    oracle bit for bit: padded leading dimensions, ragged tiles (M, N not
+    multiples of its 64 x 256 tiles), alpha and beta, every layout."""
+    rng = np.random.default_rng(7 + op_a + 2 * op_b)
+    M, N, K = 67, 300, 129
+    lda, ldb, ldc = (M if op_a else K) + 3, (K if op_b else N) + 5, N + 2
+    cv = {"f32": lambda x: x, "f16": oracle.f2h_rne, "bf16": oracle.f2bf_rne}
+    A = cv[ab](rng.uniform(-1, 1, lda * (K if op_a else M)).astype(np.float32))
+    B = cv[ab](rng.uniform(-1, 1, ldb * (N if op_b else K)).astype(np.float32))
+    C1 = cv[ct](rng.uniform(-1, 1, ldc * M).astype(np.float32))
+    C2 = C1.copy()
+    oracle.ref_gemm_epi_rm(ab, ct, op_a, op_b, M, N, K, A, lda, B, ldb, 0.75, -0.5, C1, ldc, C1, ldc)
+    oracle.ref_gemm_tiled_rm(ab, ct, op_a, op_b, M, N, K, A, lda, B, ldb, 0.75, -0.5, C2, ldc)
+    assert np.array_equal(C1.view(np.uint8), C2.view(np.uint8))
+    # and a planted mistake is seen: one k dropped from every sum
+    C3 = cv[ct](np.zeros(ldc * M, np.float32))
+    oracle.ref_gemm_tiled_rm(ab, ct, op_a, op_b, M, N, K - 1, A, lda, B, ldb, 0.75, 0.0, C3, ldc)
+    C4 = cv[ct](np.zeros(ldc * M, np.float32))
+    oracle.ref_gemm_tiled_rm(ab, ct, op_a, op_b, M, N, K, A, lda, B, ldb, 0.75, 0.0, C4, ldc)
+    assert not np.array_equal(C3.view(np.uint8), C4.view(np.uint8))

@@ -43,6 +43,20 @@ static uint32_t g_force_split = 0; /* VKBLAS_SPLITK = n (applies when split_k ==
 static int g_no_skinny = 0;     /* VKBLAS_NO_SKINNY = 1 */
 static int g_generic_only = 0;  /* VKBLAS_KERNEL = generic */
 static int g_profile = 0;       /* VKBLAS_PROFILE */
+/* The reference's own path knobs, honoured under their names:
+ *   VKBLAS_TILE128=0|1 (src/vkblas.c:914-919): 64x64 | 128x128 tiles (as
+ *     VKBLAS_TILE=64|128, which wins when both are set);
+ *   VKBLAS_NOSPLITK (any value, src/vkblas.c:2858): no split-K the planner
+ *     chooses itself (a caller's split still runs);
+ *   VKBLAS_HSPLITK=0 (src/vkblas.c:1637): the same for fp16 / bf16 only;
+ *   VKBLAS_HT256=0|1 (src/vkblas.c:1356): fp16 / bf16 GEMMs never | always
+ *     on the largest tile (256x256 here, where the pipelined kernel takes it;
+ *     the reference's largest half tile was 128x256).
+ * VKBLAS_M_SPLITK (the reference's skinny K split, src/vkblas.c:2309) is not
+ * honoured: each decode kernel here takes the split its plan derives. */
+static int g_no_split = 0;      /* VKBLAS_NOSPLITK */
+static int g_no_split16 = 0;    /* VKBLAS_HSPLITK=0 */
+static int g_ht256 = -1;        /* VKBLAS_HT256: -1 planner, 0 never, 1 always */
 
 static pthread_mutex_t g_pool_lock = PTHREAD_MUTEX_INITIALIZER;
 static hipMemPool_t g_pool[VKB_MAX_DEVICES];
@@ -53,10 +67,15 @@ static __thread int g_last_kernel = VKBLAS_KERNEL_NONE;
 static void init_once(void) {
     const char* e;
     g_trace = (e = getenv("VKBLAS_TRACE")) != NULL && e[0] && e[0] != '0';
+    if ((e = getenv("VKBLAS_TILE128")) != NULL && (e[0] == '0' || e[0] == '1') && e[1] == '\0')
+        g_force_tile = e[0] == '1' ? VKB_TILE_128 : VKB_TILE_64;
     if ((e = getenv("VKBLAS_TILE")) != NULL) {
         int v = atoi(e);
         g_force_tile = v == 64 ? VKB_TILE_64 : v == 128 ? VKB_TILE_128 : v == 256 ? VKB_TILE_256 : -1;
     }
+    g_no_split = getenv("VKBLAS_NOSPLITK") != NULL;
+    g_no_split16 = (e = getenv("VKBLAS_HSPLITK")) != NULL && e[0] == '0';
+    if ((e = getenv("VKBLAS_HT256")) != NULL && (e[0] == '0' || e[0] == '1')) g_ht256 = e[0] - '0';
     if ((e = getenv("VKBLAS_SPLITK")) != NULL) {
         long v = atol(e);
         g_force_split = v > 0 ? (uint32_t)v : 0;
@@ -366,6 +385,7 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
      * rejected.  BLAS-style ld >= rows checks live in the hipBLAS shim. */
     if (lda == 0 || ldb == 0 || ldc == 0) return VKBLAS_ERR_PARAM;
     if (split_k == 0 && g_force_split) split_k = g_force_split;
+    if (split_k == 0 && (g_no_split || (g_no_split16 && ab_type != VKBLAS_DT_F32))) split_k = 1;
 
     /* decode-shaped: X[M, K] (K-contiguous rows) against a weight W.
      * fp16 / bf16: M <= 64, W stored N x K (op_b = T) or K x N (op_b = N);
@@ -429,6 +449,10 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
         if (ab_type != VKBLAS_DT_F32 && tile == VKB_TILE_128 && t256 > 128 &&
             pipe_ok(ab_type, VKB_TILE_256, op_a, op_b, M, N, K, lda, ldb, aligned))
             tile = VKB_TILE_256;
+        if (ab_type != VKBLAS_DT_F32 && g_ht256 == 1 &&
+            pipe_ok(ab_type, VKB_TILE_256, op_a, op_b, M, N, K, lda, ldb, aligned))
+            tile = VKB_TILE_256;
+        if (ab_type != VKBLAS_DT_F32 && g_ht256 == 0 && tile == VKB_TILE_256) tile = VKB_TILE_128;
     }
     uint32_t split = 1;
     if (batch == 1) {
