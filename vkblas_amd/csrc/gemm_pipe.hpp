@@ -80,6 +80,15 @@
 namespace vkb {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Lane id within the wave, computed by instructions the compiler cannot
+// merge with an earlier computation (a fresh value where keeping the old one
+// live would cost registers).
+__device__ __forceinline__ int fresh_lane_id() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -478,7 +487,9 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             const int buf = sub < 0 ? (NSUB - 1) & 1 : sub & 1;
             mfma_unit(buf, q);
             read_one((sub + 1) & 1, S, sub + 1, q);
-            if (next) dma_unit(kt + NST - 1, (S + NST - 1) % NST, u, prev);
+            // the step is clamped for the 16-bit two-stage loop, whose last
+            // region re-reads step nkt - 1 into the idle stage (below)
+            if (next) dma_unit(min(kt + NST - 1, nkt - 1), (S + NST - 1) % NST, u, prev);
             __builtin_amdgcn_sched_barrier(0);
         }
         sync_vm(wc);
@@ -536,10 +547,14 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
             // in VGPRs, ~100 extra VALU per two K steps).  The fp32 shape
             // keeps the constant stages (its LDS addresses fold into
             // immediates) and shows no such copies.
+            // The last two regions run in the loop too: as separate code the
+            // allocator gave them their own accumulator registers, with AGPR
+            // moves and 1-10 spilled VGPRs (scratch writes on every call).
+            // The last region's copy re-reads step nkt - 1 (from L2) into the
+            // stage no later read uses; its end-of-region wait retires that
+            // copy before the epilogue reuses the LDS.
 #pragma clang loop unroll(disable)
-            for (; kt + 2 < nkt; ++kt) region(kt, kt & 1, true, true, W0{});
-            region(kt, kt & 1, true, true, W0{});             // kt == nkt - 2: loads step nkt-1
-            region(kt + 1, (kt + 1) & 1, true, false, W0{});
+            for (; kt < nkt; ++kt) region(kt, kt & 1, true, true, W0{});
         } else {
             for (; kt + 3 < nkt; kt += 2) {
                 region(kt, 1, true, true, W0{});
@@ -556,6 +571,13 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
     // ---- epilogue: C = alpha * acc (+ beta * C) ----
     // 16x16 tiles: lane holds n = 4 (lane / 16) + e of row m = lane % 16;
     // 32x32 tiles: register 4 q + e holds n = 8 q + 4 h + e of row m = l32.
+    // The lane-derived indices are recomputed here from v_mbcnt (volatile
+    // asm, so not merged with the prologue's): kept live across the K loop
+    // instead, two of them were spilled to scratch on every call.
+    {
+    const int lane = fresh_lane_id();
+    const int h = lane >> 5;
+    const int fl = SH == 0 ? (lane & 15) : (lane & 31);
     float alpha, beta;
     load_scalars(p, alpha, beta);
     constexpr int NQ = SH == 0 ? 1 : 4;
@@ -670,6 +692,7 @@ __global__ __launch_bounds__(256, (WT == 128 || NST == 4) ? 1 : 2) void gemm_pip
                 }
             }
         }
+    }
     }
 }
 
