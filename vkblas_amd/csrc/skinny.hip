@@ -738,7 +738,9 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
                 for (int c = 0; c < 4; ++c)
                     acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(x[t][e], w[e][c], acc[t][c], 0, 0, 0);
     };
-    // full chunks, the next chunk's loads in flight
+    // full chunks, the next chunk's loads in flight.  (Walking them from a
+    // rotated chunk, as skinny_nh_kernel does, measured 1-7 % slower here at
+    // 4096 x 14336, 14336 x 4096 and 4096^2, 2-3 % faster at 8192^2 n <= 8.)
     const int nf = f_end - c_beg;
     int ch = c_beg;
     {
@@ -898,25 +900,29 @@ __global__ __launch_bounds__(64 * WV) void skinny_nh_kernel(SkParams p, float* p
             for (int t = 0; t < MT; ++t) acc[t][c] = mfma16<T>(x[t], b, acc[t][c]);
         }
     };
-    // full chunks, the next chunk's loads in flight
+    // full chunks, the next chunk's loads in flight.  Each workgroup walks
+    // them from a chunk rotated by its position in the grid: the workgroups
+    // of one K slice (every column block) then read different weight rows at
+    // a time instead of the same ones.  Streaming probe (8192^2 fp16, three
+    // weights rotated): 6.0 -> 6.5 TB/s; this kernel, same box, A/B: 8192^2
+    // n = 1 / 8 / 16 27.2 / 27.7 / 28.1 -> 24.7 / 25.1 / 25.5 us, 4096^2
+    // 11.5-12.6 -> 10.4-11.6, 14336 x 4096 (K x N) -1 %, 4096 x 14336 +1-2 %.
     const int nf = f_end - c_beg;
-    int ch = c_beg;
+    const int rot = nf > 0 ? (int)((blockIdx.x * 7u + blockIdx.y * 3u) % (uint32_t)nf) : 0;
+    auto cidx = [&](int i) { return c_beg + (i + rot < nf ? i + rot : i + rot - nf); };
     {
         u32x4 wa[8], xa[MT], wb[8], xb[MT];
         int i = 0;
-        if (nf > 0) load(ch, wa, xa);
+        if (nf > 0) load(cidx(0), wa, xa);
         for (; i + 1 < nf; i += 2) {
-            load(ch + 1, wb, xb);
+            load(cidx(i + 1), wb, xb);
             mma(wa, xa);
-            if (i + 2 < nf) load(ch + 2, wa, xa);
+            if (i + 2 < nf) load(cidx(i + 2), wa, xa);
             mma(wb, xb);
-            ch += 2;
         }
-        if (i < nf) {
-            mma(wa, xa);
-            ++ch;
-        }
+        if (i < nf) mma(wa, xa);
     }
+    int ch = f_end;
     // the partial last chunk, k past K zero in both operands
     for (; ch < c_end; ++ch) {
         const int k = ch * 32 + 8 * g;
