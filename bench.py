@@ -297,6 +297,34 @@ def mfma_ceiling(torch, vk, stream, steps):
     return res
 
 
+def copy_ceiling(torch, vk, stream, steps):
+    """The rate at which a CU copies GEMM operand tiles from L2 into LDS
+    (vkblas_copy_probe: the 256x256 fp16 tile's buffer -> LDS copies at 4096^3
+    with no compute), with one step of copies in flight (waited for at each
+    step's end, as the two-stage GEMM kernel) or two, rows of 128 bytes (the
+    GEMM kernel's) or 64, on 256 workgroups (one per CU) or fewer.  The copies
+    of a 4096^3 (2048^3) 16-bit GEMM on 256x256 (128x128) tiles are 4 MiB (1
+    MiB) per CU: this rate bounds how fast they can be done."""
+    from vkblas_amd import bench_probe as probe
+    n = 4096
+    g = torch.Generator(device="cuda:0").manual_seed(19)
+    A = (torch.randn(n * n, device="cuda:0", generator=g) / 64.0).half()
+    B = (torch.randn(n * n, device="cuda:0", generator=g) / 64.0).half()
+    out = torch.empty(256, device="cuda:0", dtype=torch.int32)
+    sp = stream.cuda_stream
+    res = {}
+    for d, rb, blocks in ((1, 128, 256), (2, 128, 256), (2, 64, 256), (2, 128, 64), (2, 128, 8)):
+        def call(i):
+            probe.copy_probe(A.data_ptr(), B.data_ptr(), n, blocks, d, rb, out.data_ptr(), stream=sp)
+        warm(torch, call)
+        med = batch_ms(torch, stream, call, max(steps, 20))
+        nbytes = blocks * n * 2 * 256 * 2          # every K step of A and B rows of each tile
+        res[f"inflight{d}_row{rb}_wg{blocks}"] = {"us": round(med * 1e3, 2),
+                                                  "GBps_per_cu": round(nbytes / blocks / (med * 1e-3) / 1e9, 1),
+                                                  "TBps": round(nbytes / (med * 1e-3) / 1e12, 2)}
+    return res
+
+
 def cpu_baseline(budget_s=12.0):
     """The reference's CPU GEMM (test/test_gemm.c:32-58, restated in
     oracle/ref_gemm.c) on the headline workload, NN, parallel over output
@@ -386,7 +414,8 @@ def main():
         print(json.dumps(vendor(torch, vk, stream, args.steps)))
         return
     if args.only == "ceiling":
-        print(json.dumps(mfma_ceiling(torch, vk, stream, args.steps)))
+        print(json.dumps({"mfma": mfma_ceiling(torch, vk, stream, args.steps),
+                          "copy": copy_ceiling(torch, vk, stream, args.steps)}))
         return
     if args.only == "calibrate":
         print(json.dumps(calibrate(torch, stream)))
@@ -429,6 +458,8 @@ def main():
     line["fp16_gemm_4096"] = fp16_gemm(torch, vk, stream, args.steps, f32_out=True)
     log("[bench] MFMA rate without memory traffic (power-limited ceiling of the 16-bit legs)")
     line["mfma_ceiling"] = mfma_ceiling(torch, vk, stream, args.steps)
+    log("[bench] L2 -> LDS copy rate without compute (the 16-bit GEMMs' copy ceiling)")
+    line["copy_ceiling"] = copy_ceiling(torch, vk, stream, args.steps)
     log("[bench] fp16 matvec 8192x8192")
     line["fp16_matvec_8192"] = matvec(torch, vk, stream, args.steps)
     log("[bench] bf16 4096^3")
