@@ -544,8 +544,8 @@ def vendor(torch, vk, stream, steps):
     """The same workloads through PyTorch's own GEMM backend (hipBLASLt on
     gfx950), timed like the vkblas legs: fp32 / fp16 / bf16 4096^3 (row-major
     a @ b and a @ b.t(), i.e. hipBLAS NN and TN), the `shapes` leg's GEMMs
-    (a @ b) and 8192x8192 fp16 decode x @ w.t() with three weight copies
-    rotated.  Not part of the default run: the comparison in DESIGN.md comes
+    (a @ b) and 8192x8192 fp16 decode x @ w.t() and x @ w with three weight
+    copies rotated.  Not part of the default run: the comparison in DESIGN.md comes
     from here (plain, and with libvkblas_hipblas.so under LD_PRELOAD)."""
     n = 4096
     g = torch.Generator(device="cuda:0").manual_seed(7)
@@ -580,6 +580,15 @@ def vendor(torch, vk, stream, steps):
         med = batch_ms(torch, stream, lambda i: x @ Ws[i % 3].t(), 3 * max(steps, 10))
         nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
         out[f"decode_8192_n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
+    # x @ w with w stored K x O (row-major [K, O], hipBLAS NN)
+    Wk = [w.t().contiguous() for w in Ws]
+    del Ws
+    for nt in (1, 8, 16, 32):
+        x = X[:nt]
+        warm(torch, lambda i: x @ Wk[i % 3])
+        med = batch_ms(torch, stream, lambda i: x @ Wk[i % 3], 3 * max(steps, 10))
+        nbytes = 2 * O * K + 2 * K * nt + 2 * O * nt
+        out[f"decodeKxO_8192_n{nt}"] = {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
     return out
 
 
