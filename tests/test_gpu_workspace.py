@@ -9,7 +9,8 @@
   * Two host threads launching split-K calls on ONE stream at once: a call
     keeps its stream's buffer until its reduce is queued, so every result
     equals the call made alone, bit for bit.
-  * vkblas_workspace_release, then more calls.
+  * vkblas_workspace_release, then more calls; and from a third thread while
+    two threads issue split-K calls that grow their buffers.
 
 The split-K contract is the reference's two-pass scheme (src/vkblas.c:1873-1984,
 src/shaders/splitk_reduce_f32.comp:15-24); its partials were grow-only
@@ -217,6 +218,66 @@ def test_workspace_release_then_reuse():
     _run_splitk(vk, dA, dB, c1, M, N, K, None)
     assert np.array_equal(_bits(c1), want)
     vk.workspace_release()
+    vk.workspace_release()
+
+
+def test_workspace_release_during_calls():
+    """vkblas_workspace_release from one thread while two others issue
+    split-K calls whose partials grow their streams' buffers: the release
+    takes each slot's lock before the pool lock, as the calls do, so every
+    thread finishes (bounded joins) and every result equals the call made
+    alone."""
+    import vkblas_amd as vk
+    print("[case] workspace release during split-K calls", flush=True)
+    M, N, K = 128, 128, 16384
+    A = torch.from_numpy(_u(940, M * K)).to("cuda:0")
+    B = torch.from_numpy(_u(941, K * N)).to("cuda:0")
+    splits = (4, 16, 64)
+    alone = {}
+    for sp in splits:
+        c = torch.empty(M * N, dtype=torch.float32, device="cuda:0")
+        vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, vk.OP_N, M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(), N, 0.0,
+                      c.data_ptr(), N, split_k=sp)
+        alone[sp] = _bits(c)
+    calls = 18
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    outs = [[torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda:0") for _ in range(calls)]
+            for _ in range(2)]
+    torch.cuda.synchronize()
+    errors = []
+    done = threading.Event()
+
+    def worker(t):
+        try:
+            for i in range(calls):
+                vk.gemm_async(vk.DT_F32, vk.DT_F32, vk.OP_N, vk.OP_N, M, N, K, 1.0, A.data_ptr(), K, B.data_ptr(),
+                              N, 0.0, outs[t][i].data_ptr(), N, split_k=splits[i % 3],
+                              stream=streams[t].cuda_stream)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    def releaser():
+        try:
+            while not done.is_set():
+                vk.workspace_release()
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    rel = threading.Thread(target=releaser, daemon=True)
+    ths = [threading.Thread(target=worker, args=(t,), daemon=True) for t in range(2)]
+    rel.start()
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join(timeout=60)
+    done.set()
+    rel.join(timeout=60)
+    assert not any(th.is_alive() for th in ths + [rel]), "a thread did not finish"
+    assert not errors
+    torch.cuda.synchronize()
+    for t in range(2):
+        for i in range(calls):
+            assert np.array_equal(_bits(outs[t][i]), alone[splits[i % 3]])
     vk.workspace_release()
 
 

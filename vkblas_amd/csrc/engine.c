@@ -271,8 +271,12 @@ vkblas_status_t vkblas_workspace_release(void) {
     int cur = 0;
     if (hipGetDevice(&cur) != hipSuccess) return VKBLAS_ERR_INIT;
     vkblas_status_t st = VKBLAS_OK;
+    /* A slot's lock before g_pool_lock, the order ws_acquire takes them in.
+     * Slots below g_nws stay claimed, so the count read here stays valid. */
     pthread_mutex_lock(&g_pool_lock);
-    for (int i = 0; i < g_nws; ++i) {
+    const int nws = g_nws;
+    pthread_mutex_unlock(&g_pool_lock);
+    for (int i = 0; i < nws; ++i) {
         ws_slot_t* s = &g_ws[i];
         pthread_mutex_lock(&s->lock);
         if (s->ptr) {
@@ -280,12 +284,15 @@ vkblas_status_t vkblas_workspace_release(void) {
             if (hipSetDevice(s->dev) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
                 hipFreeAsync(s->ptr, NULL) != hipSuccess || hipStreamSynchronize(NULL) != hipSuccess)
                 st = VKBLAS_ERR_INIT;
+            pthread_mutex_lock(&g_pool_lock);
             g_ws_total -= s->bytes;
+            pthread_mutex_unlock(&g_pool_lock);
             s->ptr = NULL;
             s->bytes = 0;
         }
         pthread_mutex_unlock(&s->lock);
     }
+    pthread_mutex_lock(&g_pool_lock);
     for (int d = 0; d < VKB_MAX_DEVICES && d < g_ndev; ++d)
         if (g_pool[d] && (hipSetDevice(d) != hipSuccess || hipMemPoolTrimTo(g_pool[d], 0) != hipSuccess))
             st = VKBLAS_ERR_INIT;
