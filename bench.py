@@ -44,26 +44,6 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-class Timer:
-    """HIP events recorded on the stream the library launches on."""
-
-    def __init__(self, torch, stream):
-        self.torch, self.stream = torch, stream
-        self.pairs = []
-
-    def run(self, fn):
-        t = self.torch
-        s, e = t.cuda.Event(enable_timing=True), t.cuda.Event(enable_timing=True)
-        s.record(self.stream)
-        fn()
-        e.record(self.stream)
-        self.pairs.append((s, e))
-
-    def times_ms(self):
-        self.torch.cuda.synchronize()
-        return [s.elapsed_time(e) for s, e in self.pairs]
-
-
 WARM_MS = 20.0
 
 
@@ -133,24 +113,32 @@ def fp32_headline(torch, vk, stream, steps, warmup):
         for v in variants:
             call(*v)
     torch.cuda.synchronize()
-    timer = Timer(torch, stream)
+    # One HIP event pair around the whole timed region, on the launch stream:
+    # an event recorded between two launches of this kernel delays the next
+    # launch by about 10 us (kernel trace: 0 us between back-to-back launches,
+    # 10.2 us median with an event pair around every launch).
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    s_ev.record(stream)
     for _ in range(steps):
         for v in variants:
-            timer.run(lambda v=v: call(*v))
+            call(*v)
+    e_ev.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = timer.times_ms()
+    launches = 4 * steps
+    avg_ms = s_ev.elapsed_time(e_ev) / launches
     path = vk.PATH_NAMES[vk.last_path()]
     flops = 2.0 * n ** 3
+    # per variant, after the timed region: back-to-back launches of one
+    # variant between one event pair (batch_ms)
     by_variant = {}
-    for i, (ta, tb) in enumerate(variants):
-        ts = sorted(per[i::4])
-        by_variant["NT"[ta] + "NT"[tb]] = round(flops / (ts[len(ts) // 2] * 1e-3) / 1e12, 2)
-    avg_ms = sum(per) / len(per)
+    for ta, tb in variants:
+        ms = batch_ms(torch, stream, lambda i, ta=ta, tb=tb: call(ta, tb), max(steps, 10), batches=3)
+        by_variant["NT"[ta] + "NT"[tb]] = round(flops / (ms * 1e-3) / 1e12, 2)
     abi.hipblasDestroy(handle)
-    return {"wall_s": wall, "flops": flops * 4 * steps, "avg_launch_ms": avg_ms, "path": path,
-            "tflops_by_variant": by_variant, "launches": len(per)}
+    return {"wall_s": wall, "flops": flops * launches, "avg_launch_ms": avg_ms, "path": path,
+            "tflops_by_variant": by_variant, "launches": launches}
 
 
 def fp16_gemm(torch, vk, stream, steps, n=4096, bf16=False, f32_out=False):
