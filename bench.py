@@ -455,8 +455,8 @@ def main():
     log("[bench] bf16 matvec 8192x8192")
     line["bf16_matvec_8192"] = matvec(torch, vk, stream, args.steps, ntoks=(1, 8), bf16=True)
     log("[bench] fp16 2048^3 and 8192^3")
-    line["fp16_gemm_2048"] = fp16_gemm(torch, vk, stream, args.steps, n=2048)
-    line["fp16_gemm_8192"] = fp16_gemm(torch, vk, stream, args.steps, n=8192)
+    line["fp16_gemm_2048"] = fp16_gemm(torch, vk, stream, args.steps, n=2048, f32_out=True)
+    line["fp16_gemm_8192"] = fp16_gemm(torch, vk, stream, args.steps, n=8192, f32_out=True)
     log("[bench] decode 4096x14336 / 14336x4096")
     line["fp16_matvec_4096x14336"] = matvec(torch, vk, stream, args.steps, K=4096, O=14336, ntoks=(1, 4, 8, 16))
     line["fp16_matvec_14336x4096"] = matvec(torch, vk, stream, args.steps, K=14336, O=4096, ntoks=(1, 4, 8, 16))
