@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
 # averaged over the four variants), scaled by what the same counters read
 # for a 256 MiB device copy (FETCH x2.00, WRITE x1.00).  Summary:
 # profiles/hbm_traffic_bench_legs.txt.
-TRAFFIC_F32_4096_BYTES = int((2.00 * 197027.5 + 1.00 * 65544.8) * 1024)
+TRAFFIC_F32_4096_BYTES = int((2.00 * 196933.1 + 1.00 * 65558.2) * 1024)
 
 METRIC = "TFLOPS 4096³ fp32/fp16 GEMM (% MFMA peak); fp16 matvec GB/s (% HBM peak)"
 
