@@ -349,8 +349,8 @@ def cpu_baseline(budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--only", choices=["fp32", "fp16", "bf16", "matvec", "matvec_ns", "bf16mv", "f32mv", "splitk", "batched",
                                        "shapes", "calibrate", "ceiling", "vendor"],
                     default=None)
