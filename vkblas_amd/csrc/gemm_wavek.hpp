@@ -304,6 +304,43 @@ __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) mfma_sub(buf, s);
     };
+    // fp32: the MFMAs of sub-step s (mfma_sub's order) with the DMA
+    // instructions [d0, d1) of step jj (into stage st; instruction d copies
+    // operand A for even d, B for odd, its instruction d / 2) spread evenly
+    // among them, each MFMA and its companions fenced by a sched_barrier.  A
+    // step's DMA issued in one burst backs up in the texture address unit and
+    // holds the wave's MFMA issue meanwhile.
+    auto mfma_sub_dma = [&](int buf, int s, bool dma_on, int jj, int st, int d0, int d1) {
+        if constexpr (!F16) {
+            constexpr int NM = 4 * NF * NF;   // MFMAs per sub-step
+            const int nd = d1 - d0;
+            int k = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < NF; ++i)
+#pragma unroll
+                    for (int jt = 0; jt < NF; ++jt) {
+                        acc[e % NC][i][jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            __uint_as_float(fb[buf][s][jt][e]), __uint_as_float(fa[buf][s][i][e]),
+                            acc[e % NC][i][jt], 0, 0, 0);
+                        if (dma_on) {
+#pragma unroll
+                            for (int d = 0; d < ND; ++d)
+                                if (d >= d0 && d < d1 && (d - d0) * NM >= k * nd && (d - d0) * NM < (k + 1) * nd)
+                                    dma_op((d & 1) == 0, jj, st, d >> 1);
+                        }
+                        ++k;
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+        }
+    };
+    // fp32: the DMA of one step spread over the first DS sub-steps of another
+    auto mfma_step_dma = [&](int buf, int ds, bool dma_on, int jj, int st) {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+            mfma_sub_dma(buf, s, dma_on, jj, st, s < ds ? (ND * s) / ds : ND, s < ds ? (ND * (s + 1)) / ds : ND);
+    };
 
     // ---- K loop: step j in stage j % S; the DMA of step j + S - 1 goes
     // into the stage step j - 1 used (its fragments were consumed by the
@@ -322,14 +359,29 @@ __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
         // arrays in scratch).  The sched_barrier keeps the MFMAs of step j,
         // and so the waits for the fragments they read, ahead of the DMA
         // that next overwrites step j's stage.
+        // fp32 issues the DMA of step j + S - 1 spread over the four
+        // sub-steps of step j, after the wait and the reads of step j + 1
+        // (issued before it, step j + S - 2 may stay in flight: one step
+        // fewer than with the burst first).  Measured (M = N = 256, K = 65536,
+        // split 4, 32x32 tiles, pass 1 alone, one box): 97.4 -> 85.1 us (the
+        // DMA over the first one / two sub-steps: 90.4 / 87.2); 16-bit level
+        // (fp16 35.2 -> 34.6-35.0 us), so it keeps the burst.
         auto body = [&](int j, auto cur) {
             constexpr int C = decltype(cur)::value;
-            if (j + S - 1 < n) dma_step(j + S - 1, (j + S - 1) % S);
-            if (j + 1 < n) {
-                wait_steps(min(S - 2, n - 2 - j));
-                read_step(C ^ 1, (j + 1) % S);
+            if constexpr (F16) {
+                if (j + S - 1 < n) dma_step(j + S - 1, (j + S - 1) % S);
+                if (j + 1 < n) {
+                    wait_steps(min(S - 2, n - 2 - j));
+                    read_step(C ^ 1, (j + 1) % S);
+                }
+                mfma_step(C);
+            } else {
+                if (j + 1 < n) {
+                    wait_steps(min(S - 3, n - 2 - j));
+                    read_step(C ^ 1, (j + 1) % S);
+                }
+                mfma_step_dma(C, NSUB, j + S - 1 < n, j + S - 1, (j + S - 1) % S);
             }
-            mfma_step(C);
             __builtin_amdgcn_sched_barrier(0);
         };
 #pragma clang loop unroll(disable)
@@ -338,17 +390,28 @@ __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
             if (j + 1 < n) body(j + 1, std::integral_constant<int, 1>{});
         }
     } else {
-        // two stages: the DMA of step j + 1 goes out at the start of step j,
-        // which then waits for its own step and reads its fragments (reading
-        // them one sub-step ahead instead, the first of step j + 1 during the
-        // last of step j: fp16 M = N = 256, split 16, 19.2 -> 22.1 us; fp32
-        // unchanged)
+        // two stages.  16-bit: the DMA of step j + 1 goes out at the start of
+        // step j, which then waits for its own step and reads its fragments
+        // (reading them one sub-step ahead instead, the first of step j + 1
+        // during the last of step j: fp16 M = N = 256, split 16, 19.2 -> 22.1
+        // us).  fp32: step j waits for its own DMA (issued during step j - 1),
+        // reads its fragments, and spreads the DMA of step j + 1 over its
+        // first two sub-steps, which leaves the last two for that DMA to land.
+        // Measured (M = N = 256, K = 65536, split 16, 64x64 tiles, pass 1
+        // alone, one box): 75.5-77.7 -> 68.0-70.4 us (over one sub-step 69.9-
+        // 70.8, over all four 73.9); fp16 the same way 18.8-19.6 -> 22.6 us.
 #pragma clang loop unroll(disable)
         for (int j = 0; j < n; ++j) {
-            if (j + 1 < n) dma_step(j + 1, (j + 1) & 1);
-            wait_steps(j + 1 < n ? 1 : 0);
-            read_step(0, j & 1);
-            mfma_step(0);
+            if constexpr (F16) {
+                if (j + 1 < n) dma_step(j + 1, (j + 1) & 1);
+                wait_steps(j + 1 < n ? 1 : 0);
+                read_step(0, j & 1);
+                mfma_step(0);
+            } else {
+                wait_steps(0);
+                read_step(0, j & 1);
+                mfma_step_dma(0, 2, j + 1 < n, j + 1, (j + 1) & 1);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     }
