@@ -543,24 +543,30 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
     // the workgroups of a K slice walk it from rotated starts, so they do
     // not all read the same column range of their rows at once
     const int rot = n > 0 ? (int)((blockIdx.x * 7u) % (uint32_t)n) : 0;
-    auto copy_step = [&](int i, int stage) {
+    auto step_kb = [&](int i) {
         const int q0 = i + rot;
-        const int kb = __builtin_amdgcn_readfirstlane((s_beg + (q0 >= n ? q0 - n : q0)) * 256);
-        uint8_t* st = lds + stage * STG;
-#pragma unroll
-        for (int q = 0; q < 4 * R; ++q) {
+        return __builtin_amdgcn_readfirstlane((s_beg + (q0 >= n ? q0 - n : q0)) * 256);
+    };
+    // copy d of a step (d < 4 R: four weight rows, else four activation rows)
+    auto copy_one = [&](int d, int kb, uint8_t* st) {
+        if (d < 4 * R) {
             const int m0 = __builtin_amdgcn_readfirstlane(
-                (int)(uint32_t)(uintptr_t)(st + (wave * 16 * R + 4 * q) * 256));
-            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(vw[q]), "s"(rw), "s"(kb), "{m0}"(m0)
+                (int)(uint32_t)(uintptr_t)(st + (wave * 16 * R + 4 * d) * 256));
+            asm volatile("buffer_load_dwordx4 %0, %1, %2 offen nt lds" ::"v"(vw[d]), "s"(rw), "s"(kb), "{m0}"(m0)
                          : "memory");
-        }
-#pragma unroll
-        for (int q = 0; q < MT; ++q) {
+        } else {
+            const int q = d - 4 * R;
             const int m0 = __builtin_amdgcn_readfirstlane(
                 (int)(uint32_t)(uintptr_t)(st + (WROWS + wave * 4 * MT + 4 * q) * 256));
             asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(vx[q]), "s"(rx), "s"(kb), "{m0}"(m0)
                          : "memory");
         }
+    };
+    auto copy_step = [&](int i, int stage) {
+        const int kb = step_kb(i);
+        uint8_t* st = lds + stage * STG;
+#pragma unroll
+        for (int d = 0; d < NQ; ++d) copy_one(d, kb, st);
     };
 
     floatx4 acc[R][MT];
@@ -579,7 +585,19 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
         if (later == 0) asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         else if (later == 1) asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(NQ) : "memory");
         else asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(2 * NQ) : "memory");
-        if (i + S - 1 < n) copy_step(i + S - 1, stage == 0 ? S - 1 : stage - 1);
+        // 16-bit: the copies of step i + S - 1 go out in one burst here.
+        // fp32 (MFMA-bound from 33 rows): they go out among the first half of
+        // this step's MFMAs, each product fenced by a sched_barrier: in one
+        // burst they back up in the texture address unit and hold the wave's
+        // MFMA issue.  Measured (8192^2, weight N x K, three weights rotated,
+        // one box, two runs): fp32 32 / 64 rows 52.5-53.0 / 86.7-86.9 ->
+        // 50.6-51.7 / 78.0-78.8 us (over all the MFMAs: 50.1-50.5 / 80.0-
+        // 80.4); fp16 24-64 rows within 0.5 % either way.
+        const bool cp = i + S - 1 < n;
+        const int cstage = stage == 0 ? S - 1 : stage - 1;
+        if constexpr (sizeof(T) != 4) {
+            if (cp) copy_step(i + S - 1, cstage);
+        }
         const uint8_t* st = lds + stage * STG;
         u32x4 wf[R][4], xf[MT][4];
 #pragma unroll
@@ -590,12 +608,35 @@ __global__ __launch_bounds__(256) void decode_lds_kernel(SkParams p, float* part
 #pragma unroll
             for (int t = 0; t < MT; ++t) xf[t][j] = *(const u32x4*)(st + (WROWS + 16 * t + l16) * 256 + slot);
         }
+        if constexpr (sizeof(T) != 4) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+                for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int t = 0; t < MT; ++t) acc[r][t] = mfma_frag<T>(wf[r][j], xf[t][j], acc[r][t]);
+                    for (int t = 0; t < MT; ++t) acc[r][t] = mfma_frag<T>(wf[r][j], xf[t][j], acc[r][t]);
+        } else {
+            const int kb = cp ? step_kb(i + S - 1) : 0;
+            uint8_t* stc = lds + cstage * STG;
+            constexpr int NP = 4 * R * MT;   // fragment products per step
+            int k = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int t = 0; t < MT; ++t) {
+                        acc[r][t] = mfma_frag<T>(wf[r][j], xf[t][j], acc[r][t]);
+                        if (cp) {
+                            // copy d goes with product floor(d NP / (2 NQ))
+#pragma unroll
+                            for (int d = 0; d < NQ; ++d)
+                                if (d * NP >= k * 2 * NQ && d * NP < (k + 1) * 2 * NQ) copy_one(d, kb, stc);
+                        }
+                        ++k;
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+        }
         stage = stage + 1 == S ? 0 : stage + 1;
     }
     if (tail) {   // partial last K step, zero-filled beyond K
