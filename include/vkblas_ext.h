@@ -196,9 +196,10 @@ int vkblas_last_kernel(void);
  * hipMalloc).  Same arguments, plan, kernels and results as
  * vkblas_gemm_async; the split-K and split-decode partials ([split][M][N]
  * fp32) go to a fixed per-device scratch array of
- * vkblas_noalloc_scratch_bytes() (64 MiB) instead of an allocated
- * workspace.  A call whose partials need more returns VKBLAS_ERR_PARAM
- * before launching anything (e.g. split_k = 128 on a 1024 x 1024 output).
+ * vkblas_noalloc_scratch_bytes() (64 MiB of partials after 4 KiB of split-K
+ * arrival counters) instead of an allocated workspace.  A call whose
+ * partials need more returns VKBLAS_ERR_PARAM before launching anything
+ * (e.g. split_k = 128 on a 1024 x 1024 output).
  * All calls on one device share its array: calls that overlap in time on
  * one device (other streams, unordered threads) race and must be ordered by
  * the caller.

@@ -393,9 +393,9 @@ def test_plan_forced_split(K, split, dt):
     assert pl.split * pl.k_per_split >= K > (pl.split - 1) * pl.k_per_split
     assert pl.split == split
     # 64 slices of the four 128x128 tiles fill the CUs: the pipelined
-    # 128x128 kernel; 16 slices of 64x64 tiles or 4 of 32x32 (tile code 3)
-    # do on the wave-K kernel
-    assert pl.tile == {64: 1, 16: 0, 4: 3}[split]
+    # 128x128 kernel; 16 slices of 64x64 tiles, or 4 slices of 64x64 tiles
+    # each over four workgroups (tile code 4), do on the wave-K kernel
+    assert pl.tile == {64: 1, 16: 0, 4: 4}[split]
 
 
 def test_plan_split_heuristic_and_off():
@@ -497,11 +497,12 @@ def test_launcher_rejects_pointer_array_with_separate_c(dt):
 def test_plan_caller_split_small_tiles():
     """A caller's split whose 128x128 tiles give fewer than 224 workgroups:
     split-K pass 1 on 64x64 tiles (the wave-K kernel) when they give at least
-    224, else on 32x32 tiles (tile code 3); M = N = 256 at BASELINE
-    configs[4]'s splits 4 / 16 / 64."""
+    224; else on 64x64 tiles with each K slice over four workgroups (tile code
+    4) when that gives 224 and the slices are at least 16 K steps long; else
+    on 32x32 tiles (tile code 3).  M = N = 256 at BASELINE configs[4]'s splits 4 / 16 / 64."""
     for dt in (vk.DT_F32, vk.DT_F16, vk.DT_BF16):
         for K in (65536, 262144):
-            for split, tile in ((4, 3), (16, 0), (64, 1)):
+            for split, tile in ((4, 4), (16, 0), (64, 1)):
                 pl = P(dt, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256, split_k=split)
                 assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, split, tile), (dt, K, split, pl.tile)
     # ragged for 64x64 but whole 32x32 tiles: 32x32
@@ -514,7 +515,12 @@ def test_plan_caller_split_small_tiles():
     pl = P(vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 8288, 8288, 256, 256, split_k=4)
     assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 8288, 8288, 256, 256, split_k=4)
-    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 3)
+    assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 4)
+    # slices too short to divide (fewer than 16 K steps of 32 k): 32x32
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 2048, 2048, 256, 256, split_k=4)
+    assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 4, 4)
+    pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 1024, 1024, 256, 256, split_k=4)
+    assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, 4, 3)
     # unaligned operands: no wave-K plan either
     pl = P(vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, 8192, 8192, 256, 256, split_k=4, aligned=False)
     assert (pl.path, pl.tile) == (vk.PATH_SPLITK, 0)

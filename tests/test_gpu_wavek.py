@@ -42,10 +42,11 @@ def _ref(dt, op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc):
         oracle.ref_gemm_bf16f32_rm(op_a, op_b, M, N, K, A, lda, B, ldb, alpha, beta, C, ldc)
 
 
-# (M, N, K, split, expected tile edge): 64x64 tiles where they give >= 224
-# workgroups, else 32x32
-SHAPES = [(256, 256, 8256, 4, 32), (256, 256, 8192, 16, 64), (64, 128, 3008, 3, 32), (192, 96, 4096, 5, 32),
-          (512, 256, 2048, 8, 64)]
+# (M, N, K, split, expected tile code): 64x64 tiles (0) where they give >=
+# 224 workgroups; else 64x64 tiles with each K slice over four workgroups (4)
+# where that gives 224 and the slices hold at least 16 K steps; else 32x32 (3)
+SHAPES = [(256, 256, 8256, 4, 4), (256, 256, 8192, 16, 0), (64, 128, 3008, 3, 3), (192, 96, 4096, 5, 3),
+          (512, 256, 2048, 8, 0), (256, 256, 1024, 4, 3), (128, 256, 16384, 9, 4)]
 
 
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
@@ -63,8 +64,7 @@ def test_wavek_layouts(dt, op_a, op_b, shape):
     code = {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}[dt]
     pl = vk.plan(code, vk.DT_F32, op_a, op_b, M, N, K, lda, ldb, N, split_k=split)
     assert pl.path == vk.PATH_SPLITK and pl.split == split
-    edge = 32 if pl.tile == 3 else 64 << pl.tile
-    assert edge == tt, (pl.tile, tt)
+    assert pl.tile == tt, (pl.tile, tt)
     dA, dB = _dev(hA, dt), _dev(hB, dt)
     outs = []
     for _ in range(2):
@@ -110,3 +110,37 @@ def test_wavek_epilogue(dt, split):
     bound = f32_bound(K) if dt == "f32" else F16_BOUND
     assert normwise(to_host(dD), want) <= bound
 
+
+def test_wavek_divided_slices_repeat():
+    """Each K slice over four workgroups (the last to arrive adds the four
+    sums): calls of three shapes interleaved on one stream, each repeated,
+    give the first call's result bit for bit (the arrival counters stay in
+    step across calls and shapes), and the oracle's within the bound."""
+    import vkblas_amd as vk
+    from gpu_helpers import to_host, normwise, f32_bound
+    print("[case] wavek divided slices, repeated", flush=True)
+    cases = [(256, 256, 16384, 4), (128, 256, 16384, 9), (256, 256, 8256, 5)]
+    data = []
+    for i, (M, N, K, split) in enumerate(cases):
+        pl = vk.plan(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, K, N, N, split_k=split)
+        assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, split, 4), (M, N, K, split, pl.tile)
+        hA, hB = _u(50 + i, M * K), _u(60 + i, K * N)
+        data.append((hA, hB, torch.from_numpy(hA).to("cuda:0"), torch.from_numpy(hB).to("cuda:0")))
+    first = {}
+    for rep in range(3):
+        for i, (M, N, K, split) in enumerate(cases):
+            _, _, dA, dB = data[i]
+            dC = torch.full((M * N,), float("nan"), dtype=torch.float32, device="cuda:0")
+            vk.gemm_async(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(), N, 0.0,
+                          dC.data_ptr(), N, split_k=split)
+            assert vk.last_kernel() == vk.KERNEL_WAVEK
+            got = to_host(dC)
+            if rep == 0:
+                first[i] = got
+            else:
+                assert np.array_equal(got.view(np.uint32), first[i].view(np.uint32)), (rep, cases[i])
+    for i, (M, N, K, split) in enumerate(cases):
+        hA, hB, _, _ = data[i]
+        ref = np.zeros(M * N, np.float32)
+        oracle.ref_gemm_f32_rm(0, 0, M, N, K, hA, K, hB, N, 1.0, 0.0, ref, N)
+        assert normwise(first[i], ref) <= f32_bound(K), cases[i]

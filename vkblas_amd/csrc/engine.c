@@ -168,12 +168,25 @@ typedef struct {
     hipStream_t stream;
 } ws_lease_t;
 
+/* A workspace starts with VKB_WS_HEADER bytes of arrival counters, zero
+ * when the buffer is new (the partials follow; see vkb_launch.h).  Never
+ * called under stream capture: a capturing stream gets no workspace. */
+static int ws_clear_header(void* p, hipStream_t stream) {
+    return hipMemsetAsync(p, 0, VKB_WS_HEADER, stream) == hipSuccess ? 0 : -1;
+}
+
 static int ws_owned(hipStream_t stream, size_t bytes, hipMemPool_t pool, ws_lease_t* L) {
     if (hipMallocFromPoolAsync(&L->ptr, bytes, pool, stream) != hipSuccess) {
         L->ptr = NULL;
         return -1;
     }
     L->owned = 1;
+    if (ws_clear_header(L->ptr, stream) != 0) {
+        hipFreeAsync(L->ptr, stream);
+        L->ptr = NULL;
+        L->owned = 0;
+        return -1;
+    }
     return 0;
 }
 
@@ -242,7 +255,8 @@ static int ws_acquire(hipStream_t stream, size_t bytes, ws_lease_t* L) {
         return ws_owned(stream, bytes, pool, L);
     }
     void* p = NULL;
-    if (hipMallocFromPoolAsync(&p, want, pool, stream) != hipSuccess) {
+    if (hipMallocFromPoolAsync(&p, want, pool, stream) != hipSuccess || ws_clear_header(p, stream) != 0) {
+        if (p) hipFreeAsync(p, stream);
         pthread_mutex_lock(&g_pool_lock);
         g_ws_total = g_ws_total + s->bytes - want;
         pthread_mutex_unlock(&g_pool_lock);
@@ -472,11 +486,23 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
                 (uint64_t)cdiv(M, 128) * cdiv(N, 128) * split_k >= 224 && K / split_k >= PIPE_MIN_STEPS * bk)
                 tile = VKB_TILE_128;
             /* fewer: the wave-K kernel on 64x64 tiles if they give at least
-             * 224 workgroups, else on 32x32 tiles (M = N = 256: split 16 ->
-             * 256 workgroups of 64x64, split 4 -> 256 of 32x32) */
+             * 224 workgroups; else on 64x64 tiles with each K slice over
+             * VKB_WAVEK_NQ workgroups if that gives 224 (slices of at least
+             * 4 K steps per workgroup); else on 32x32 tiles.  M = N = 256:
+             * split 16 -> 256 workgroups of 64x64, split 4 -> 256 of 64x64
+             * in quarter slices.  Split 4, whole call, 32x32 tiles against
+             * quarter slices (bench.py --only splitk, two boxes): K = 65536
+             * fp32 87.5-88.2 -> 74.2-74.5 us, fp16 36.3-37.2 -> 20.3-20.6 us;
+             * K = 262144 fp32 344.4-344.8 -> 270.6-271.0 us, fp16 133.2-
+             * 133.6 -> 68.5-69.2 us. */
             else if (g_force_tile < 0 && wavek_ok(ab_type, 64, op_a, op_b, M, N, K, lda, ldb, aligned) &&
                      (uint64_t)(M / 64) * (N / 64) * split_k >= 224)
                 tile = VKB_TILE_64;
+            else if (g_force_tile < 0 && wavek_ok(ab_type, 64, op_a, op_b, M, N, K, lda, ldb, aligned) &&
+                     (uint64_t)(M / 64) * (N / 64) * split_k * VKB_WAVEK_NQ >= 224 &&
+                     (uint64_t)(M / 64) * (N / 64) * split_k <= VKB_WS_COUNTERS &&
+                     K / split_k >= VKB_WAVEK_NQ * 4u * (ab_type == VKBLAS_DT_F32 ? 32u : 64u))
+                tile = VKB_TILE_64Q;
             else if (g_force_tile < 0 && wavek_ok(ab_type, 32, op_a, op_b, M, N, K, lda, ldb, aligned))
                 tile = VKB_TILE_32;
         } else if (split_k == 0 && g_force_tile < 0 && pipe_ok(ab_type, VKB_TILE_128, op_a, op_b, M, N, K, lda, ldb, aligned) &&
@@ -562,9 +588,9 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
             plan->k_per_split = kps;
             return VKBLAS_OK;
         }
-        /* no split left (K within one slice): 32x32 tiles exist only for
-         * split-K pass 1 */
-        if (tile == VKB_TILE_32) tile = choose_tile(M, N, batch);
+        /* no split left (K within one slice): 32x32 tiles and divided
+         * slices exist only for split-K pass 1 */
+        if (tile == VKB_TILE_32 || tile == VKB_TILE_64Q) tile = choose_tile(M, N, batch);
     }
     /* A partial last wave: with T tiles on `slots` concurrent workgroups
      * (one 256x256 or two 128x128 per CU on 256 CUs), T = W slots + R and
@@ -712,13 +738,18 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
                 op_a ? "T" : "N", op_b ? "T" : "N", type_name(ab), type_name(ct), M, N, K, lda, ldb, ldc, batch,
                 path_name(plan.path), plan.split, ws_ext ? " (scratch)" : "");
 
-    /* partials: [split][M][N] fp32 for split-K and the split decode kernel,
-     * [split][tail_rows][N] for the split tail */
+    /* workspace: the arrival counters (VKB_WS_HEADER bytes), then the
+     * partials: [split][M][N] fp32 for split-K and the split decode kernel,
+     * [split][tail_rows][N] for the split tail; with divided K slices
+     * (VKB_TILE_64Q) then the parts' sums, VKB_WAVEK_NQ x the partials */
     int partials = plan.split > 1 && (plan.path == VKBLAS_PATH_SKINNY || plan.path == VKBLAS_PATH_SPLITK ||
                                       plan.path == VKBLAS_PATH_TAIL);
-    size_t ws_bytes = partials ? (size_t)plan.split * (plan.path == VKBLAS_PATH_TAIL ? plan.tail_rows : M) * N *
-                                     sizeof(float)
-                               : 0;
+    const size_t part_bytes =
+        partials ? (((size_t)plan.split * (plan.path == VKBLAS_PATH_TAIL ? plan.tail_rows : M) * N * sizeof(float) +
+                     255) & ~(size_t)255)
+                 : 0;
+    const int divided = partials && plan.path == VKBLAS_PATH_SPLITK && plan.tile == VKB_TILE_64Q;
+    size_t ws_bytes = partials ? VKB_WS_HEADER + part_bytes * (divided ? 1 + VKB_WAVEK_NQ : 1) : 0;
     /* The planner's own K splits (split-K for few output tiles, the split
      * tail) only speed a call up: where their partials have no room (the
      * caller's scratch is smaller; a capturing stream declines the
@@ -738,7 +769,7 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
         if (!room) ws_release(&lease);
         ws = lease.ptr;
     }
-    if (!room && optional &&
+    if (!room && optional && !divided &&
         vkblas_plan_gemm(ab_type, c_type, op_a, op_b, M, N, K, lda, ldb, ldc, batch, 1, aligned, &plan) ==
             VKBLAS_OK &&
         plan.split == 1) {
@@ -757,13 +788,13 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
         return ws_ext ? VKBLAS_ERR_PARAM : VKBLAS_ERR_INIT;
     }
 
+    float* part = partials ? (float*)((char*)ws + VKB_WS_HEADER) : NULL;
     if (plan.path == VKBLAS_PATH_SKINNY) {
         /* decode; with a K split over workgroups: fp32 partials, fixed-order reduce */
         rc = vkb_launch_skinny(ab, op_b == VKBLAS_OP_T, A, lda, B, ldb, C, ldc, ct, M, N, K, alpha, beta,
-                               (int)scalar_mode, alpha_dev, beta_dev, epp, partials ? (float*)ws : NULL,
-                               partials ? plan.split : 1, stream);
+                               (int)scalar_mode, alpha_dev, beta_dev, epp, part, partials ? plan.split : 1, stream);
         if (rc == 0 && partials)
-            rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
+            rc = vkb_launch_splitk_reduce(part, (int64_t)M * N, plan.split, M, N, C, ldc, ct, alpha, beta,
                                           (int)scalar_mode, alpha_dev, beta_dev, epp, stream);
     } else {
         vkb_gemm_args a;
@@ -798,7 +829,7 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
             vkb_gemm_args t = a;
             t.M = plan.tail_rows;
             t.A = (const char*)A + (size_t)head * (op_a == VKBLAS_OP_N ? (size_t)lda : 1) * es_ab;
-            t.C = ws;
+            t.C = part;
             t.ldc = N;
             t.c_type = VKB_T_F32;
             t.split = plan.split;
@@ -820,12 +851,16 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
                 if (tep.c_in) tep.c_in = (const char*)tep.c_in + (size_t)head * tep.ldc_in * es_c;
             }
             if (rc == 0)
-                rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)plan.tail_rows * N, plan.split,
+                rc = vkb_launch_splitk_reduce(part, (int64_t)plan.tail_rows * N, plan.split,
                                               plan.tail_rows, N, (char*)C + (size_t)head * ldc * es_c, ldc, ct,
                                               alpha, beta, (int)scalar_mode, alpha_dev, beta_dev,
                                               epp ? &tep : NULL, stream);
         } else if (plan.path == VKBLAS_PATH_SPLITK) {
-            a.C = ws;
+            a.C = part;
+            if (divided) {
+                a.qcnt = (uint32_t*)ws;
+                a.qpart = (float*)((char*)part + part_bytes);
+            }
             a.ldc = N;
             a.stride_c = 0;
             a.c_type = VKB_T_F32;
@@ -838,7 +873,7 @@ static vkblas_status_t gemm_impl(vkblas_dtype_t ab_type, vkblas_dtype_t c_type, 
             a.epi = NULL;
             rc = vkb_launch_gemm(&a, plan.tile, stream);
             if (rc == 0)
-                rc = vkb_launch_splitk_reduce((const float*)ws, (int64_t)M * N, plan.split, M, N, C, ldc, ct,
+                rc = vkb_launch_splitk_reduce(part, (int64_t)M * N, plan.split, M, N, C, ldc, ct,
                                               alpha, beta, (int)scalar_mode, alpha_dev, beta_dev, epp, stream);
         } else {
             rc = vkb_launch_gemm(&a, plan.tile, stream);

@@ -65,11 +65,12 @@ template <typename T, typename TC>
 static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     constexpr int VEC = Elem<T>::VEC;
     constexpr int BK = Elem<T>::BK;
+    static_assert(WAVEK_NQ == VKB_WAVEK_NQ, "one part count");
     int bm = 64, bn = 64;
     if (tile == VKB_TILE_128) { bm = bn = 128; }
     else if (tile == VKB_TILE_256) { bm = bn = 256; }
     else if (tile == VKB_TILE_32) { bm = bn = 32; }
-    else if (tile != VKB_TILE_64) return (int)hipErrorInvalidValue;
+    else if (tile != VKB_TILE_64 && tile != VKB_TILE_64Q) return (int)hipErrorInvalidValue;
 
     KParams p{};
     p.A = a->A; p.B = a->B; p.C = a->C;
@@ -94,6 +95,14 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     p.epi.bias_type = ep ? ep->bias_type : 0;
     p.ptr_array = a->ptr_array != 0;
     if (p.ptr_array && sep_cin) return (int)hipErrorInvalidValue;   // Cin pointers are not given
+    // each K slice over VKB_WAVEK_NQ workgroups: the wave-K kernel only (below)
+    p.nq = tile == VKB_TILE_64Q ? VKB_WAVEK_NQ : 1;
+    p.qpart = a->qpart;
+    p.qcnt = a->qcnt;
+    if (tile == VKB_TILE_64Q &&
+        (p.split < 2 || p.ptr_array || !a->qpart || !a->qcnt || ((uintptr_t)a->qpart & 15) ||
+         ((uintptr_t)a->qcnt & 3) || (uint64_t)p.split * p.tiles_m * p.tiles_n > VKB_WS_COUNTERS))
+        return (int)hipErrorInvalidValue;
     const bool multi = p.batch > 1;
     if (p.ptr_array) {
         // the matrices' alignment is checked per batch in the kernel, which
@@ -125,7 +134,7 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
 
     const bool full = !p.ptr_array && (a->M % bm == 0) && (a->N % bn == 0) && (a->K % BK == 0) &&
                       p.vec_a && p.vec_b && p.vec_c;
-    const uint64_t grid64 = (uint64_t)p.tiles_m * p.tiles_n * p.batch * p.split;
+    const uint64_t grid64 = (uint64_t)p.tiles_m * p.tiles_n * p.batch * p.split * p.nq;
     if (grid64 == 0 || grid64 > 0x7fffffffull) return (int)hipErrorInvalidValue;
     const uint32_t grid = (uint32_t)grid64;
     const bool ak = a->a_kmajor != 0, bk = a->b_kmajor != 0;
@@ -195,7 +204,8 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
     // slice's K.  Whole tiles, K and the slice in whole K steps, aligned
     // operands; buffer offsets are signed 32-bit.
     if constexpr (std::is_same<TC, float>::value) {
-        if ((tile == VKB_TILE_32 || tile == VKB_TILE_64) && p.split > 1 && !p.ptr_array && !a->generic_only) {
+        if ((tile == VKB_TILE_32 || tile == VKB_TILE_64 || tile == VKB_TILE_64Q) && p.split > 1 && !p.ptr_array &&
+            !a->generic_only) {
             constexpr uint64_t ES = sizeof(T);
             const uint32_t tt = (uint32_t)bm;
             const uint64_t span_a = ((uint64_t)(ak ? tt : a->K) * (uint64_t)a->lda + a->K) * ES;
@@ -225,7 +235,8 @@ static int launch_gemm_typed(const vkb_gemm_args* a, int tile, hipStream_t st) {
             }
         }
     }
-    if (tile == VKB_TILE_32) return (int)hipErrorInvalidValue;   // only the wave-K kernel takes 32x32 tiles
+    // only the wave-K kernel takes 32x32 tiles or divided slices
+    if (tile == VKB_TILE_32 || tile == VKB_TILE_64Q) return (int)hipErrorInvalidValue;
     report(full ? VKB_KERN_GENERIC : VKB_KERN_GENERIC_CHECKED);
     switch (tile) {
         case VKB_TILE_64:  return launch_layout<T, TC, VKB_TILE_64>(p, ak, bk, !full, grid, st);

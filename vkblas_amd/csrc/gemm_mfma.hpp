@@ -67,6 +67,11 @@ struct KParams {
     // strides are unused); vec_* then also need each matrix aligned, which
     // the kernel checks per batch
     int ptr_array;
+    // wave-K split-K pass 1 with each K slice over nq workgroups (nq > 1):
+    // their sums in qpart, their arrival counters in qcnt
+    uint32_t nq;
+    float* qpart;
+    uint32_t* qcnt;
 };
 
 template <typename T> struct Elem;

@@ -75,6 +75,10 @@ struct WaveKGeom {
     static constexpr int ND = 2 * NDO;
 };
 
+// Workgroups per (slice, tile) when a launch divides each K slice (KParams
+// nq > 1; the launcher passes 1 or this).
+constexpr int WAVEK_NQ = 4;
+
 template <typename T, bool AK, bool BKM, int TT, int KB16 = 64>
 __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
     using G = WaveKGeom<T, TT, KB16>;
@@ -97,15 +101,20 @@ __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
     const uint32_t nwg = gridDim.x;
     if ((nwg & 7u) == 0) bid = (bid & 7u) * (nwg >> 3) + (bid >> 3);
     const uint32_t per = p.tiles_m * p.tiles_n;
-    const uint32_t b = bid / per;
-    const uint32_t t = bid - b * per;
+    const uint32_t nq = p.nq > 1 ? WAVEK_NQ : 1;  // workgroups per (slice, tile)
+    const uint32_t bq = bid / per;                // slice b, part q: bq = b nq + q
+    const uint32_t t = bid - bq * per;
+    const uint32_t b = bq / nq, qi = bq - b * nq;
     const int m0 = (int)(t / p.tiles_n) * TT, n0 = (int)(t % p.tiles_n) * TT;
-    // slice b: k in [b kps, min(K, (b + 1) kps)); wave w takes its steps
-    // [ns w / 4, ns (w + 1) / 4)
+    // slice b: k in [b kps, min(K, (b + 1) kps)), nsl steps; part q takes
+    // steps [nsl q / nq, nsl (q + 1) / nq) of them, ns in all, and wave w
+    // the steps [ns w / 4, ns (w + 1) / 4) of those
     const int64_t kbeg = (int64_t)b * p.kps;
     const uint32_t klen = min(p.K - (uint32_t)kbeg, p.kps);
-    const int ns = (int)(klen / KS);
-    const int s0 = (ns * wave) >> 2, n = ((ns * (wave + 1)) >> 2) - s0;
+    const int nsl = (int)(klen / KS);
+    const int qs0 = (int)(((uint32_t)nsl * qi) / nq);
+    const int ns = (int)(((uint32_t)nsl * (qi + 1)) / nq) - qs0;
+    const int s0 = qs0 + ((ns * wave) >> 2), n = ((ns * (wave + 1)) >> 2) - ((ns * wave) >> 2);
     const int64_t kw = kbeg + (int64_t)s0 * KS;
     const int lda = (int)p.lda, ldb = (int)p.ldb;
     const T* At = (const T*)p.A + (AK ? (int64_t)m0 * p.lda + kw : kw * p.lda + m0);
@@ -446,17 +455,68 @@ __global__ __launch_bounds__(256, 1) void gemm_wavek_kernel(KParams p) {
     constexpr int V4 = TT / 4;                 // float4 per row
     constexpr int PER = (TT / 4) * V4 / 64;    // float4 per lane
     float* Cp = (float*)p.C + (int64_t)b * p.s_split;
+    floatx4 sum[PER];
 #pragma unroll
     for (int it = 0; it < PER; ++it) {
         const int e = it * 64 + lane;
         const int r = wave * (TT / 4) + e / V4, c = e % V4;
-        floatx4 sum = *(const floatx4*)((const char*)lds + r * RS + c * 16);
+        sum[it] = *(const floatx4*)((const char*)lds + r * RS + c * 16);
 #pragma unroll
         for (int w = 1; w < 4; ++w) {
             const floatx4 v = *(const floatx4*)((const char*)lds + w * WU * 16 + r * RS + c * 16);
-            sum += v;
+            sum[it] += v;
         }
-        *(floatx4*)(Cp + (int64_t)(m0 + r) * p.ldc + n0 + 4 * c) = sum;
+    }
+    if (nq == 1) {
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int e = it * 64 + lane;
+            const int r = wave * (TT / 4) + e / V4, c = e % V4;
+            *(floatx4*)(Cp + (int64_t)(m0 + r) * p.ldc + n0 + 4 * c) = sum[it];
+        }
+        return;
+    }
+    // Part q of nq: store the sum (row-major TT x TT) where the other parts
+    // of this slice and tile will read it, with device-scope coherent stores
+    // (sc1: through the XCD's L2, which another XCD does not see), wait for
+    // them, then count this workgroup's arrival.  The last of the nq to
+    // arrive reads the nq sums back (device-scope coherent loads), adds them
+    // in part order and writes the slice's partial: the same order whatever
+    // the order of arrival, so the partials are bitwise reproducible.  The
+    // counter gains nq per launch and starts each launch at a multiple of nq.
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(p.qpart + (int64_t)(b * per + t) * nq * (TT * TT)), (short)0, -1, 0x00020000);
+    constexpr int SC1 = 16;   // cache policy: sc1 (device scope)
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+        const int e = it * 64 + lane;
+        const int r = wave * (TT / 4) + e / V4, c = e % V4;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[it]), rq,
+                                               (int)((qi * (TT * TT) + r * TT + 4 * c) * 4), 0, SC1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ uint32_t q_last;
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(p.qcnt + b * per + t, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        q_last = old % nq == nq - 1;
+    }
+    __syncthreads();
+    if (!q_last) return;
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+        const int e = it * 64 + lane;
+        const int r = wave * (TT / 4) + e / V4, c = e % V4;
+        floatx4 v[WAVEK_NQ];
+#pragma unroll
+        for (int q = 0; q < WAVEK_NQ; ++q)
+            v[q] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(rq, (q * (TT * TT) + r * TT + 4 * c) * 4, 0, SC1));
+        floatx4 tot = v[0];
+#pragma unroll
+        for (int q = 1; q < WAVEK_NQ; ++q) tot += v[q];
+        *(floatx4*)(Cp + (int64_t)(m0 + r) * p.ldc + n0 + 4 * c) = tot;
     }
 }
 

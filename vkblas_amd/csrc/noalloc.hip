@@ -13,18 +13,25 @@
 // the first call there, and kept per device.
 //
 // Every call on a device shares that device's array and finds it holding
-// the previous call's partials.  Nothing in it needs to start at zero: pass
-// 1 of split-K and the decode kernel write every partial the reduce then
-// reads.  Calls on one device that overlap in time (different streams, or
-// different threads without ordering) race on the array; order them.
+// the previous call's partials.  The partials need no clearing: pass 1 of
+// split-K and the decode kernel write every partial the reduce then reads.
+// The array's first VKB_WS_HEADER bytes are the arrival counters of split-K
+// passes that divide each K slice among workgroups; they must start at zero
+// (each such launch then adds the same multiple to every counter it uses),
+// so the first call on a device clears them with a fill kernel on its stream
+// (no hipMemsetAsync: the call may be under stream capture).  Calls on one
+// device that overlap in time (different streams, or different threads
+// without ordering) race on the array; order them.
 #include <hip/hip_runtime.h>
 #include <pthread.h>
 #include <stdint.h>
 
 #include "vkb_engine.h"
+#include "vkb_launch.h"
 #include "vkblas_ext.h"
 
-#define VKB_SCRATCH_BYTES ((size_t)64 << 20)
+// 64 MiB of partials after the VKB_WS_HEADER bytes of arrival counters
+#define VKB_SCRATCH_BYTES (((size_t)64 << 20) + VKB_WS_HEADER)
 
 static __device__ __align__(256) unsigned char scratch[VKB_SCRATCH_BYTES];
 
@@ -34,12 +41,24 @@ constexpr int kMaxDevices = 64;
 pthread_mutex_t g_scratch_lock = PTHREAD_MUTEX_INITIALIZER;
 void* g_scratch_ptr[kMaxDevices];
 
-// Device address of `scratch` on the current device (dev), or NULL.
-void* scratch_on(int dev) {
+__global__ void clear_words(uint32_t* p, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device (dev), or NULL.  The
+// first call on a device also enqueues the clearing of the counters on
+// `stream`, ahead of the call's own kernels.
+void* scratch_on(int dev, hipStream_t stream) {
     pthread_mutex_lock(&g_scratch_lock);
     void* p = g_scratch_ptr[dev];
     if (!p) {
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) p = nullptr;
+        if (p) {
+            hipLaunchKernelGGL(clear_words, dim3(VKB_WS_COUNTERS / 256), dim3(256), 0, stream, (uint32_t*)p,
+                               (uint32_t)VKB_WS_COUNTERS);
+            if (hipGetLastError() != hipSuccess) p = nullptr;
+        }
         g_scratch_ptr[dev] = p;
     }
     pthread_mutex_unlock(&g_scratch_lock);
@@ -58,7 +77,7 @@ extern "C" vkblas_status_t vkblas_gemm_noalloc_async(
     void* stream) {
     int dev = -1;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return VKBLAS_ERR_INIT;
-    void* s = scratch_on(dev);
+    void* s = scratch_on(dev, (hipStream_t)stream);
     if (!s) return VKBLAS_ERR_INIT;
     return vkb_gemm_with_scratch(ab_type, c_type, op_a, op_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, batch,
                                  stride_a, stride_b, stride_c, scalar_mode, alpha_dev, beta_dev, split_k, stream, s,

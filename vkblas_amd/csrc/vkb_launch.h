@@ -43,10 +43,23 @@ enum {
     VKB_TILE_128 = 1,  /* 128 x 128, waves 2x2 of  64x64 */
     VKB_TILE_256 = 2,  /* 256 x 256, waves 2x2 of 128x128 */
     VKB_TILE_COUNT = 3,
-    VKB_TILE_32 = 3    /* 32 x 32, split-K pass 1 only (gemm_wavek_kernel:
+    VKB_TILE_32 = 3,   /* 32 x 32, split-K pass 1 only (gemm_wavek_kernel:
                           each wave the whole tile over a quarter of the
                           slice's K); not a choice for unsplit GEMMs */
+    VKB_TILE_64Q = 4   /* 64 x 64, split-K pass 1 only (gemm_wavek_kernel),
+                          each K slice divided among VKB_WAVEK_NQ workgroups
+                          per output tile whose sums the last of them to
+                          finish adds in a fixed order (vkb_gemm_args.qpart) */
 };
+
+/* Workgroups sharing one K slice of a 64 x 64 tile under VKB_TILE_64Q. */
+#define VKB_WAVEK_NQ 4
+/* Every partials workspace (split-K, split decode) starts with this many
+ * bytes of 32-bit arrival counters for VKB_TILE_64Q, zeroed when the
+ * workspace is allocated; the partials follow.  Each VKB_TILE_64Q launch
+ * adds VKB_WAVEK_NQ to every counter it uses, so they stay multiples of it. */
+#define VKB_WS_HEADER 4096u
+#define VKB_WS_COUNTERS (VKB_WS_HEADER / 4u)
 
 /* Optional epilogue inputs (every launcher):
  *   C = alpha * acc + beta * C_in + bias[n]
@@ -93,6 +106,13 @@ typedef struct vkb_gemm_args {
     /* optional epilogue inputs (NULL: in place, no bias); unused by split-K
      * pass 1, whose raw partials take no epilogue */
     const vkb_epilogue_args* epi;
+    /* tile VKB_TILE_64Q only: the VKB_WAVEK_NQ workgroups of a (slice, tile)
+     * store their 64 x 64 sums to qpart + ((slice * tiles + tile) * NQ + q)
+     * * 4096 floats and count their arrival in qcnt[slice * tiles + tile]
+     * (at most VKB_WS_COUNTERS words, each a multiple of NQ at launch); the
+     * last to arrive writes the slice's partial to C. */
+    float* qpart;
+    uint32_t* qcnt;
 } vkb_gemm_args;
 
 /* Tile-config properties the dispatcher plans with. */
