@@ -355,6 +355,8 @@ def main():
                                        "shapes", "calibrate", "ceiling", "vendor"],
                     default=None)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--splits", default="4,16,64,0",
+                    help="--only splitk: the splits to time (0: the planner's choice)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GEMM hot path has no multi-GPU path in this build "
@@ -390,7 +392,8 @@ def main():
                           "14336x4096": matvec_f32(torch, vk, stream, args.steps, K=14336, O=4096)}))
         return
     if args.only == "splitk":
-        print(json.dumps(splitk(torch, vk, stream, args.steps)))
+        splits = tuple(int(x) for x in args.splits.split(","))
+        print(json.dumps(splitk(torch, vk, stream, args.steps, splits=splits)))
         return
     if args.only == "batched":
         print(json.dumps(batched(torch, vk, stream, args.steps)))
@@ -523,7 +526,7 @@ def splitk(torch, vk, stream, steps, splits=(4, 16, 64, 0)):
                 if not split:
                     pl = vk.plan(vk.DT_F16 if dt == "f16" else vk.DT_F32, vk.DT_F32, 0, 0, 256, 256, K, K, 256, 256)
                     out[key]["split"] = pl.split
-                    out[key]["tile"] = 64 << pl.tile
+                    out[key]["tile"] = {0: 64, 1: 128, 2: 256, 3: 32, 4: 64}[pl.tile]
             del A, B
     return out
 
