@@ -60,8 +60,9 @@ typedef enum {
 
 typedef struct {
     int path;              /* vkblas_path_t                                 */
-    int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256,
-                              3:32 for split-K pass 1)                     */
+    int tile;              /* tile of the GEMM kernel (0:64, 1:128, 2:256;
+                              split-K pass 1 only: 3:32, 4:64 with each K
+                              slice divided among four workgroups)         */
     uint32_t split;        /* split-K factor, 1 = no split (VKBLAS_PATH_TAIL:
                               the split of the tail rows)                  */
     uint32_t k_per_split;  /* K per split (multiple of the tile's K step)   */
