@@ -784,7 +784,7 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
     // 4096 x 14336, 14336 x 4096 and 4096^2, 2-3 % faster at 8192^2 n <= 8.)
     const int nf = f_end - c_beg;
     int ch = c_beg;
-    {
+    if constexpr (MT == 1) {
         floatx4 wa[4], xa[MT], wb[4], xb[MT];
         int i = 0;
         if (nf > 0) load(ch, wa, xa);
@@ -799,6 +799,28 @@ __global__ __launch_bounds__(64 * WV) void skinny_n_kernel(SkParams p, float* pa
             mma(wa, xa);
             ++ch;
         }
+    } else {
+        // 17-64 rows: three chunks' loads in flight (buffer u of NB holds
+        // chunk i + u).  Measured against one chunk ahead (same box, two
+        // runs, 32 / 64 rows): 8192^2 60.3-60.5 / 87.8-87.9 -> 56.8-56.9 /
+        // 83.5 us, K x N = 4096 x 14336 57.5-57.6 / 85.2 -> 54.9-55.0 /
+        // 79.5-79.7, 14336 x 4096 54.5 / 78.3-78.7 -> 52.0-52.2 / 74.5-74.6;
+        // up to 16 rows it measured -3 to +4 % and keeps one chunk ahead.
+        constexpr int NB = 4;
+        floatx4 wv[NB][4], xv[NB][MT];
+#pragma unroll
+        for (int j = 0; j < NB - 1; ++j)
+            if (j < nf) load(c_beg + j, wv[j], xv[j]);
+        for (int i = 0; i < nf; i += NB) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                if (i + u < nf) {
+                    if (i + u + NB - 1 < nf) load(c_beg + i + u + NB - 1, wv[(u + NB - 1) % NB], xv[(u + NB - 1) % NB]);
+                    mma(wv[u], xv[u]);
+                }
+            }
+        }
+        ch = f_end;
     }
     // the partial last chunk, k past K zero
     for (; ch < c_end; ++ch) {
