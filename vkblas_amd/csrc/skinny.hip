@@ -11,8 +11,8 @@
 //   C[m][n] = alpha * sum_k X[m][k] * W[n][k] + beta * C[m][n],  m < M <= 64
 //
 // Three kernels by the number of activation rows M:
-//  * M <= 2: gemv_kernel, v_dot2 accumulation on whole-row loads;
-//  * 3 <= M <= 16: skinny_lds_kernel, one v_mfma_f32_16x16x32_{f16,bf16}
+//  * M == 1: gemv_kernel, v_dot2 accumulation on whole-row loads;
+//  * 2 <= M <= 16: skinny_lds_kernel, one v_mfma_f32_16x16x32_{f16,bf16}
 //    tile (src A = 16 weight rows, src B = up to 16 activation rows) whose
 //    operands are copied to LDS as whole lines and read back as fragments;
 //  * 17 <= M <= 64: decode_lds_kernel (16-bit types and fp32), weights and
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(64 * WAVES) void skinny_lds_kernel(SkParams p) {
 }
 
 // ---------------------------------------------------------------- GEMV
-// For M <= 2 activation rows (token-by-token decode) the MFMA tile is mostly
+// For one activation row (token-by-token decode) the MFMA tile is mostly
 // idle and its fragment layout splits every load over 16 rows (half lines).
 // Here a wave reads 1 KB of ONE weight row per instruction (8 whole 128-byte
 // lines, loaded non-temporal: the weights stream through once, and whole-line
@@ -1156,19 +1156,19 @@ int launch_dec_mt(const SkParams& p, float* part, int nsplit, hipStream_t st) {
 }
 
 // One element type: output fp32 or the input type.
-//   M <= 2: the GEMV kernel, 4 weight rows per workgroup (measured best for
+//   M == 1: the GEMV kernel, 4 weight rows per workgroup (measured best for
 //   4096-14336 rows); more activation rows multiply its VALU work and
-//   registers.
-//   3 <= M <= DEC_MIN_M - 1: skinny_lds_kernel, one 16-row tile per
-//   workgroup, four waves splitting K, two steps in flight per wave.
+//   registers.  At M = 2 the staged kernel is ahead (same box, two runs,
+//   fp16: 8192^2 23.0 -> 22.0 us, K x O = 4096 x 14336 19.6 -> 18.6,
+//   14336 x 4096 20.4 -> 18.8, 4096^2 8.0 -> 7.5; bf16 8192^2 23.2 -> 22.1);
+//   at M = 1 it is level or behind (8192^2 22.0 -> 22.3, 4096^2 7.2 -> 7.3,
+//   14336 x 4096 19.2 -> 18.7).
+//   2 <= M <= DEC_MIN_M - 1: skinny_lds_kernel (skl_plan's geometry).
 //   DEC_MIN_M <= M <= 64: decode_lds_kernel, one workgroup per CU, K split
 //   nsplit ways over the grid.
 template <typename T>
 int launch_typed(const SkParams& p, bool f32_out, float* part, int nsplit, hipStream_t st) {
-    if (p.M <= 2) {
-        if (f32_out) return p.M == 1 ? launch_gemv<T, float, 1, 4>(p, st) : launch_gemv<T, float, 2, 4>(p, st);
-        return p.M == 1 ? launch_gemv<T, T, 1, 4>(p, st) : launch_gemv<T, T, 2, 4>(p, st);
-    }
+    if (p.M == 1) return f32_out ? launch_gemv<T, float, 1, 4>(p, st) : launch_gemv<T, T, 1, 4>(p, st);
     if ((int)p.M >= DEC_MIN_M)
         return f32_out ? launch_dec_mt<T, float>(p, part, nsplit, st) : launch_dec_mt<T, T>(p, part, nsplit, st);
     return f32_out ? launch_sk_lds<T, float>(p, st) : launch_sk_lds<T, T>(p, st);
