@@ -110,3 +110,27 @@ def test_noalloc_rejects_partials_beyond_scratch():
                           dC.data_ptr(), N, split_k=8)
     torch.cuda.synchronize()
     assert torch.all(dC == 0.0)
+
+
+def test_noalloc_divided_slices_match_gemm_async():
+    """A caller's split run with each K slice divided among four workgroups
+    (their arrival counters at the start of the scratch array, cleared on the
+    device's first no-alloc call): the same bits as vkblas_gemm_async, on two
+    calls in a row, the second smaller."""
+    import vkblas_amd as vk
+    from gpu_helpers import to_host
+    print("[case] noalloc divided K slices", flush=True)
+    for M, N, K, split in ((256, 256, 16384, 4), (128, 256, 8192, 9)):
+        pl = vk.plan(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, K, N, N, split_k=split)
+        assert (pl.path, pl.split, pl.tile) == (vk.PATH_SPLITK, split, 4), (M, N, K, pl.tile)
+        a = np.random.default_rng(M + split).uniform(-1, 1, M * K).astype(np.float32)
+        b = np.random.default_rng(N + split).uniform(-1, 1, K * N).astype(np.float32)
+        dA, dB = torch.from_numpy(a).to("cuda:0"), torch.from_numpy(b).to("cuda:0")
+        c_ref = torch.full((M * N,), float("nan"), device="cuda:0")
+        c_na = torch.full((M * N,), float("nan"), device="cuda:0")
+        vk.gemm_async(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(), N, 0.0,
+                      c_ref.data_ptr(), N, split_k=split)
+        vk.gemm_noalloc_async(vk.DT_F32, vk.DT_F32, 0, 0, M, N, K, 1.0, dA.data_ptr(), K, dB.data_ptr(), N, 0.0,
+                              c_na.data_ptr(), N, split_k=split)
+        assert vk.last_kernel() == vk.KERNEL_WAVEK
+        assert np.array_equal(to_host(c_na).view(np.uint32), to_host(c_ref).view(np.uint32)), (M, N, K, split)
