@@ -43,10 +43,14 @@ CASES = [
     ("decode-f16", "f16", 0, 1, 20, 4096, 4096, "skinny"),
     ("tile-f16", "f16", 0, 0, 512, 512, 512, "tile"),
     ("tile-f16", "f16", 1, 0, 256, 256, 256, "tile"),
+    # weight K x N: the 16-bit K x N decode kernel's K split (8 and 15 slices)
+    ("decode-kn-f16", "f16", 0, 0, 16, 8192, 8192, "skinny"),
+    ("decode-kn-f16", "f16", 0, 0, 33, 2048, 8200, "skinny"),
 ]
 
 
-@pytest.mark.parametrize("pair", [0, 1, 2, 3], ids=["splitk-f16", "splitk-f32", "decode-f16", "tile-f16"])
+@pytest.mark.parametrize("pair", [0, 1, 2, 3, 4],
+                         ids=["splitk-f16", "splitk-f32", "decode-f16", "tile-f16", "decode-kn-f16"])
 def test_noalloc_matches_gemm_async(pair):
     import vkblas_amd as vk
     from gpu_helpers import normwise, f32_bound, F16_BOUND
