@@ -265,3 +265,47 @@ def test_unsupported_matmuls_are_forwarded(lt, what):
     for lay in (la, lb, ld):
         lt.ours.hipblasLtMatrixLayoutDestroy(lay)
     lt.ours.hipblasLtMatmulDescDestroy(desc)
+
+
+def _sweep_case(i):
+    """Seeded random matmul i: types, transposes, shape (decode-shaped or
+    general, aligned or ragged), padding, alpha / beta, bias (D's type or
+    fp32), C == D or a separate C, strided batch, host or device scalars."""
+    r = np.random.default_rng(40000 + i)
+    ab, dt = COMBOS[r.integers(len(COMBOS))]
+    if r.random() < 0.3:   # decode-shaped: a few columns of D (tokens) against a weight
+        m, n, k = int(r.integers(8, 4097)), int(r.integers(1, 17)), int(r.integers(8, 2049))
+    else:
+        m, n, k = int(r.integers(1, 600)), int(r.integers(1, 600)), int(r.integers(1, 1500))
+    if r.random() < 0.6:
+        m, k = -(-m // 8) * 8, -(-k // 8) * 8
+        pads = tuple(int(8 * r.integers(0, 3)) for _ in range(3))
+    else:
+        pads = tuple(int(r.integers(0, 9)) for _ in range(3))
+    bias_mode = [None, "d", "f32"][r.integers(3)]
+    if bias_mode == "f32" and dt == "f32":
+        bias_mode = "d"
+    return dict(ab=ab, dt=dt, ta=int(r.integers(2)), tb=int(r.integers(2)), m=m, n=n, k=k,
+                alpha=float(np.round(r.uniform(-2, 2), 3)),
+                beta=0.0 if r.random() < 0.5 else float(np.round(r.uniform(-1.5, 1.5), 3)),
+                bias_mode=bias_mode, sep_c=bool(r.random() < 0.3),
+                batch=int(r.integers(2, 4)) if r.random() < 0.15 else 1, pmode=int(r.random() < 0.25), pads=pads)
+
+
+SWEEP = [_sweep_case(i) for i in range(150)]
+
+
+@pytest.mark.parametrize("c", SWEEP, ids=[f"{i}" for i in range(len(SWEEP))])
+def test_matmul_random_sweep(lt, c):
+    """150 seeded random matmuls through the interposed hipblasLtMatmul, each
+    computed by this library (not forwarded) and checked against the oracle"""
+    import vkblas_amd as vk
+    # the engine's form of the call (row-major D' = op(B)' op(A)'): which
+    # path it takes decides the marker call's path
+    dt_ = {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}
+    lda = (c["k"] if c["ta"] else c["m"]) + c["pads"][0]
+    ldb = (c["n"] if c["tb"] else c["k"]) + c["pads"][1]
+    ldd = c["m"] + c["pads"][2]
+    pl = vk.plan(dt_[c["ab"]], dt_[c["dt"]], c["tb"], c["ta"], c["n"], c["m"], c["k"], ldb, lda, ldd, c["batch"])
+    run_lt(lt, c["ab"], c["dt"], c["ta"], c["tb"], c["m"], c["n"], c["k"], c["alpha"], c["beta"], c["bias_mode"],
+           c["sep_c"], batch=c["batch"], pmode=c["pmode"], pads=c["pads"], decode=pl.path == vk.PATH_SKINNY)
