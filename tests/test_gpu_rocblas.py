@@ -301,3 +301,132 @@ def test_gemm_batched_ex_ptr_array(rh, dt):
         # column-major C = A op(B)^T with B (n x k) -> engine: op_a = transB = T, op_b = transA = N
         ref(1, 0, n, m, k, Bs[i], n, As[i], m, 1.0, 0.5, want, m)
         assert normwise(dec(to_host(dC[i])), dec(want)) <= bound
+
+
+# Seeded random sweep: rocblas_gemm_ex / rocblas_gemm_strided_batched_ex with
+# every type pair the layer computes, both transposes, decode-shaped and
+# general shapes (aligned or ragged), padding, beta (0 over a NaN C), C == D
+# or a separate D, host or device scalars, strided batches; each call
+# asserted computed (a marker call on another path first) and checked
+# against the oracle (oracle.ref_gemm_epi_rm on the row-major mapping).
+RT = {"f16": F16, "f32": F32, "bf16": BF16}
+SW_TYPES = [("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "f32")]
+SW_NAN = {"f32": np.float32(np.nan), "f16": np.uint16(0x7E00), "bf16": np.uint16(0x7FC0)}
+SW_CONV = {"f32": lambda x: x.astype(np.float32), "f16": oracle.f2h_rne, "bf16": oracle.f2bf_rne}
+SW_BACK = {"f32": lambda x: x.astype(np.float32), "f16": oracle.h2f, "bf16": oracle.bf2f}
+
+
+def _sw_case(i):
+    r = np.random.default_rng(60000 + i)
+    ab, ct = SW_TYPES[r.integers(len(SW_TYPES))]
+    if r.random() < 0.3:
+        m, n, k = int(r.integers(8, 4097)), int(r.integers(1, 17)), int(r.integers(8, 2049))
+    else:
+        m, n, k = int(r.integers(1, 700)), int(r.integers(1, 700)), int(r.integers(1, 1600))
+    if r.random() < 0.6:
+        m, k = -(-m // 8) * 8, -(-k // 8) * 8
+        pads = tuple(int(8 * r.integers(0, 3)) for _ in range(4))
+    else:
+        pads = tuple(int(r.integers(0, 9)) for _ in range(4))
+    return dict(ab=ab, ct=ct, ta=int(r.integers(2)), tb=int(r.integers(2)), m=m, n=n, k=k, pads=pads,
+                alpha=float(np.round(r.uniform(-2, 2), 3)),
+                beta=0.0 if r.random() < 0.5 else float(np.round(r.uniform(-1.5, 1.5), 3)),
+                sep_d=bool(r.random() < 0.3), device=bool(r.random() < 0.25),
+                batch=int(r.integers(2, 4)) if r.random() < 0.2 else 1)
+
+
+SW_CASES = [_sw_case(i) for i in range(150)]
+
+
+def _sw_mats(r, nb, stride, rows, cols, ld, t, scale):
+    buf = np.full(nb * stride, SW_NAN[t], np.float32 if t == "f32" else np.uint16)
+    for b in range(nb):
+        vals = SW_CONV[t]((r.standard_normal(rows * cols) * scale).astype(np.float32)).reshape(rows, cols)
+        buf[b * stride: b * stride + rows * ld].reshape(rows, ld)[:, :cols] = vals
+    return buf
+
+
+@pytest.mark.parametrize("c", SW_CASES, ids=[f"{i}" for i in range(len(SW_CASES))])
+def test_gemm_ex_random_sweep(rh, c):
+    import torch
+    import vkblas_amd as vk
+    from gpu_helpers import normwise, f32_bound, F16_BOUND, BF16_BOUND
+    print(f"[case] rocblas sweep {c}", flush=True)
+    ab, ct, m, n, k, ta, tb, nb = c["ab"], c["ct"], c["m"], c["n"], c["k"], c["ta"], c["tb"], c["batch"]
+    r = np.random.default_rng(80000 + m + n + k)
+    # column-major A: m x k (k x m under T): k rows of m in row-major terms
+    a_rows, a_cols = (m, k) if ta else (k, m)
+    b_rows, b_cols = (k, n) if tb else (n, k)
+    lda, ldb, ldc, ldd = a_cols + c["pads"][0], b_cols + c["pads"][1], m + c["pads"][2], m + c["pads"][3]
+    gap = 8 if nb > 1 else 0
+    sa, sb, sc, sd = a_rows * lda + gap, b_rows * ldb + gap, n * ldc + gap, n * ldd + gap
+    A = _sw_mats(r, nb, sa, a_rows, a_cols, lda, ab, 1.0)
+    B = _sw_mats(r, nb, sb, b_rows, b_cols, ldb, ab, 0.05)
+    C = _sw_mats(r, nb, sc, n, m, ldc, ct, 1.0)
+    TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+    def dev(x, t):
+        return torch.from_numpy(x.view(np.int16) if x.dtype == np.uint16 else x).view(TD[t]).to("cuda:0")
+    gpu_c = C.copy()
+    if c["beta"] == 0.0 and not c["sep_d"]:
+        gpu_c[:] = SW_NAN[ct]
+    dA, dB, dC = dev(A, ab), dev(B, ab), dev(gpu_c, ct)
+    D0 = np.full(nb * sd, SW_NAN[ct], np.float32 if ct == "f32" else np.uint16) if c["sep_d"] else None
+    dD = dev(D0, ct) if c["sep_d"] else dC
+    ldd_ = ldd if c["sep_d"] else ldc
+    sd_ = sd if c["sep_d"] else sc
+    pl = vk.plan({"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}[ab],
+                 {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}[ct], tb, ta, n, m, k, ldb, lda, ldd_, nb)
+    # the marker: 2 rows against W stored N x K (the decode kernels) or 65
+    # against W stored K x N (a 64x64 tile), whichever this call does not take
+    x = torch.zeros(65 * 64, dtype=torch.float16, device="cuda:0")
+    w = torch.zeros(64 * 64, dtype=torch.float16, device="cuda:0")
+    y = torch.zeros(65 * 64, dtype=torch.float16, device="cuda:0")
+    rows_mk = 2 if pl.path != vk.PATH_SKINNY else 65
+    vk.gemm_async(vk.DT_F16, vk.DT_F16, 0, 1 if rows_mk == 2 else 0, rows_mk, 64, 64, 1.0, x.data_ptr(), 64,
+                  w.data_ptr(), 64, 0.0, y.data_ptr(), 64)
+    torch.cuda.synchronize()
+    marker = vk.last_path()
+    assert marker == (vk.PATH_SKINNY if rows_mk == 2 else vk.PATH_TILE64)
+    if c["device"]:
+        sc_dev = torch.tensor([c["alpha"], c["beta"]], dtype=torch.float32, device="cuda:0")
+        pa, pb = ctypes.c_void_p(sc_dev.data_ptr()), ctypes.c_void_p(sc_dev.data_ptr() + 4)
+        rh.set_pointer_mode(DEVICE)
+    else:
+        ha, hb_ = ctypes.c_float(c["alpha"]), ctypes.c_float(c["beta"])
+        pa, pb = ctypes.byref(ha), ctypes.byref(hb_)
+    try:
+        if nb == 1:
+            st = rh.lib.rocblas_gemm_ex(rh.h, OP[ta], OP[tb], m, n, k, pa, dA.data_ptr(), RT[ab], lda, dB.data_ptr(),
+                                        RT[ab], ldb, pb, dC.data_ptr(), RT[ct], ldc, dD.data_ptr(), RT[ct], ldd_, F32,
+                                        0, 0, 0)
+        else:
+            st = rh.lib.rocblas_gemm_strided_batched_ex(rh.h, OP[ta], OP[tb], m, n, k, pa, dA.data_ptr(), RT[ab], lda,
+                                                        sa, dB.data_ptr(), RT[ab], ldb, sb, pb, dC.data_ptr(), RT[ct],
+                                                        ldc, sc, dD.data_ptr(), RT[ct], ldd_, sd_, nb, F32, 0, 0, 0)
+        torch.cuda.synchronize()
+    finally:
+        if c["device"]:
+            rh.set_pointer_mode(HOST)
+    assert st == 0
+    assert vk.last_path() == pl.path != marker, "the call was forwarded"
+    got = dD.cpu()
+    got = got.view(torch.int16).numpy().view(np.uint16) if ct != "f32" else got.numpy()
+    rows = oracle.sample_rows(n, 16) if m * n * k > 64 * 1024 * 1024 else None
+    sel = np.arange(n) if rows is None else rows
+    bound = f32_bound(k) if (ab, ct) == ("f32", "f32") else (BF16_BOUND if ct == "bf16" else F16_BOUND)
+    for b in range(nb):
+        want = np.full(n * ldd_, SW_NAN[ct], got.dtype)
+        oracle.ref_gemm_epi_rm(ab, ct, tb, ta, n, m, k, np.ascontiguousarray(B[b * sb:(b + 1) * sb]), ldb,
+                               np.ascontiguousarray(A[b * sa:(b + 1) * sa]), lda, c["alpha"], c["beta"],
+                               np.ascontiguousarray(C[b * sc: b * sc + n * ldc]), ldc, want, ldd_, None, rows=rows)
+        gb = got[b * sd_: b * sd_ + n * ldd_]
+        g = SW_BACK[ct](np.stack([gb[j * ldd_: j * ldd_ + m] for j in sel]))
+        wv = SW_BACK[ct](np.stack([want[j * ldd_: j * ldd_ + m] for j in sel]))
+        assert np.all(np.isfinite(g)), f"batch {b}"
+        err = normwise(g, wv)
+        assert err <= bound, f"batch {b}: {err:.3g}"
+    if c["sep_d"]:
+        assert np.array_equal(dC.cpu().view(torch.int16 if ct != "f32" else torch.int32).numpy().view(
+            np.uint16 if ct != "f32" else np.uint32), gpu_c.view(np.uint16 if ct != "f32" else np.uint32)), \
+            "C was written"
