@@ -216,3 +216,84 @@ def test_plain_ld_preload_reference_script():
     assert not any("forwarding" in l for l in err), r.stderr[-4000:]
     # the kernels ran in the same process, on PyTorch's HIP runtime
     assert any(l.startswith("[vkblas] gemm ") and "path=skinny" in l for l in err), r.stderr[-4000:]
+
+
+# Seeded random PyTorch products under plain LD_PRELOAD: matmul of 2-D
+# tensors (contiguous or transposed views), bmm and batched matmul (right
+# operand contiguous: PyTorch's own bf16 batched path has faulted on a
+# transposed right operand on these boxes), linear with and without a bias,
+# addmm with alpha / beta and a matrix or 1-D bias, decode-shaped linear;
+# fp32, fp16 and bf16.  Each result is checked against PyTorch's CPU result
+# in float64 of the same inputs (normwise: fp32 1e-5 sqrt(K), fp16 2e-3,
+# bf16 8e-3), and no call may be forwarded to the vendor library.
+CHILD_RANDOM = r"""
+import json, math, torch
+g = torch.Generator().manual_seed(2026)
+dev = "cuda"
+out = []
+DT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+def ri(lo, hi):
+    return int(torch.randint(lo, hi + 1, (1,), generator=g))
+def rnd(*shape, dt, scale=1.0):
+    return (torch.randn(*shape, generator=g) * scale).to(DT[dt])
+def rel(got, ref):
+    torch.cuda.synchronize()
+    got = got.cpu().double(); ref = ref.double()
+    den = float(ref.abs().max())
+    return float((got - ref).abs().max()) / (den if den > 0 else 1.0)
+for i in range(120):
+    dt = ["f32", "f16", "bf16"][i % 3]
+    kind = ["mm", "mm_t", "bmm", "linear", "linear_bias", "addmm", "decode"][ri(0, 6)]
+    big = ri(0, 9) == 0
+    M, N, K = (ri(1, 3000), ri(1, 3000), ri(1, 2048)) if big else (ri(1, 400), ri(1, 400), ri(1, 600))
+    if ri(0, 1):
+        M, N, K = -(-M // 8) * 8, -(-N // 8) * 8, -(-K // 8) * 8
+    s = 1.0 / math.sqrt(K)
+    if kind == "mm":
+        a, b = rnd(M, K, dt=dt), rnd(K, N, dt=dt, scale=s)
+        got, ref = a.to(dev) @ b.to(dev), a.double() @ b.double()
+    elif kind == "mm_t":     # transposed views on either side
+        a, b = rnd(K, M, dt=dt), rnd(N, K, dt=dt, scale=s)
+        got, ref = a.to(dev).t() @ b.to(dev).t(), a.double().t() @ b.double().t()
+    elif kind == "bmm":
+        B = ri(2, 4)
+        a, b = rnd(B, M if not big else M // 8 + 1, K, dt=dt), rnd(B, K, N if not big else N // 8 + 1, dt=dt, scale=s)
+        got, ref = torch.bmm(a.to(dev), b.to(dev).contiguous()), torch.bmm(a.double(), b.double())
+    elif kind in ("linear", "linear_bias"):
+        x, w = rnd(M, K, dt=dt), rnd(N, K, dt=dt, scale=s)
+        bias = rnd(N, dt=dt) if kind == "linear_bias" else None
+        got = torch.nn.functional.linear(x.to(dev), w.to(dev), None if bias is None else bias.to(dev))
+        ref = x.double() @ w.double().t() + (0 if bias is None else bias.double())
+    elif kind == "addmm":
+        a, b = rnd(M, K, dt=dt), rnd(K, N, dt=dt, scale=s)
+        c = rnd(N, dt=dt) if ri(0, 1) else rnd(M, N, dt=dt)
+        al, be = round(float(torch.rand(1, generator=g)) * 3 - 1.5, 3), round(float(torch.rand(1, generator=g)) * 2 - 1, 3)
+        got = torch.addmm(c.to(dev), a.to(dev), b.to(dev), beta=be, alpha=al)
+        ref = be * c.double() + al * (a.double() @ b.double())
+    else:                    # decode: a few tokens against a large weight
+        T = ri(1, 16)
+        O, K2 = -(-ri(256, 8192) // 8) * 8, -(-ri(256, 4096) // 8) * 8
+        x, w = rnd(T, K2, dt=dt), rnd(O, K2, dt=dt, scale=1.0 / math.sqrt(K2))
+        got, ref = torch.nn.functional.linear(x.to(dev), w.to(dev)), x.double() @ w.double().t()
+        K = K2
+    out.append([i, kind, dt, K, rel(got, ref)])
+print("RESULT " + json.dumps(out), flush=True)
+"""
+
+
+def test_plain_ld_preload_random_products():
+    import os
+    import vkblas_amd as vk
+    old = os.environ.get("LD_PRELOAD", "")
+    env = dict(os.environ, LD_PRELOAD=":".join([vk.LIB_PATH] + ([old] if old else [])), VKBLAS_TRACE="1")
+    print("[case] plain LD_PRELOAD, 120 seeded random products", flush=True)
+    r = subprocess.run([sys.executable, "-c", CHILD_RANDOM], env=env, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-4000:]
+    res = json.loads(next(l for l in r.stdout.splitlines() if l.startswith("RESULT "))[len("RESULT "):])
+    assert len(res) == 120
+    for i, kind, dt, K, err in res:
+        bound = 8e-3 if dt == "bf16" else 2e-3 if dt == "f16" else 1e-5 * K ** 0.5
+        assert err <= bound, (i, kind, dt, K, err)
+    err_lines = r.stderr.splitlines()
+    assert not any("forwarding" in l for l in err_lines), [l for l in err_lines if "forwarding" in l][:5]
+    assert sum(l.startswith("[vkblas] gemm ") for l in err_lines) >= 120, r.stderr[-2000:]
