@@ -11,6 +11,9 @@
     equals the call made alone, bit for bit.
   * vkblas_workspace_release, then more calls; and from a third thread while
     two threads issue split-K calls that grow their buffers.
+  * Four streams fed at once by four threads with a mix of calls that need
+    partials (split-K, divided K slices with their arrival counters, split
+    decodes in both weight layouts, the split tail).
 
 The split-K contract is the reference's two-pass scheme (src/vkblas.c:1873-1984,
 src/shaders/splitk_reduce_f32.comp:15-24); its partials were grow-only
@@ -325,3 +328,70 @@ def test_heuristic_split_without_room_runs_unsplit(tmp_path):
     r = subprocess.run([sys.executable, "-c", CHILD_NO_ROOM, repo], env=env, capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 0 and "NO ROOM OK" in r.stdout, f"rc={r.returncode}\n{r.stdout[-3000:]}\n{r.stderr[-3000:]}"
+
+
+def test_four_streams_mixed_calls_at_once():
+    """Four streams, each fed by its own host thread with a different mix of
+    calls that need partials (planner split-K, a caller's split 4 with K
+    slices divided among workgroups and their arrival counters, a split
+    decode, the split tail): every stream keeps its own workspace, so every
+    result equals the same call made alone, bit for bit."""
+    import vkblas_amd as vk
+    print("[case] four streams, mixed partial-using calls", flush=True)
+    r = np.random.default_rng(950)
+    h16 = lambda n, s=1.0: torch.from_numpy(oracle.f2h_rne((r.standard_normal(n) * s).astype(np.float32))
+                                            .view(np.int16)).view(torch.float16).to("cuda:0")
+    # (label, ab, ct, op_a, op_b, M, N, K, split_k, operand scale of B)
+    calls = [("splitk", vk.DT_F16, vk.DT_F16, 0, 0, 256, 256, 16384, 0, 1.0),
+             ("divided", vk.DT_F16, vk.DT_F32, 0, 0, 256, 256, 16384, 4, 1.0),
+             ("decode", vk.DT_F16, vk.DT_F16, 0, 1, 24, 8192, 4096, 0, 0.05),
+             ("decode_kn", vk.DT_F16, vk.DT_F16, 0, 0, 16, 8192, 8192, 0, 0.05),
+             ("tail", vk.DT_F16, vk.DT_F16, 0, 0, 4608, 4096, 2048, 0, 1.0)]
+    ops = []
+    for label, ab, ct, op_a, op_b, M, N, K, sp, sc in calls:
+        lda = M if op_a else K
+        ldb = K if op_b else N
+        A, B = h16(M * K), h16(K * N, sc)
+        pl = vk.plan(ab, ct, op_a, op_b, M, N, K, lda, ldb, N, split_k=sp)
+        assert pl.split > 1 or pl.path == vk.PATH_TAIL, (label, pl.path, pl.split)
+        ops.append((label, ab, ct, op_a, op_b, M, N, K, sp, lda, ldb, A, B))
+
+    def launch(o, out, stream):
+        label, ab, ct, op_a, op_b, M, N, K, sp, lda, ldb, A, B = o
+        vk.gemm_async(ab, ct, op_a, op_b, M, N, K, 1.0, A.data_ptr(), lda, B.data_ptr(), ldb, 0.0, out.data_ptr(), N,
+                      split_k=sp, stream=stream)
+
+    def new_out(o):
+        return torch.full((o[5] * o[6],), float("nan"), dtype=torch.float32 if o[2] == vk.DT_F32 else torch.float16,
+                          device="cuda:0")
+    alone = []
+    for o in ops:
+        c = new_out(o)
+        launch(o, c, None)
+        alone.append(_bits(c))
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    rounds = 3
+    outs = [[[new_out(o) for o in ops] for _ in range(rounds)] for _ in range(4)]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(s):
+        try:
+            for rd in range(rounds):
+                for j in range(len(ops)):
+                    k = (j + s + rd) % len(ops)       # each stream its own order
+                    launch(ops[k], outs[s][rd][k], streams[s].cuda_stream)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    ths = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
+    assert not errors, errors
+    torch.cuda.synchronize()
+    for s in range(4):
+        for rd in range(rounds):
+            for k in range(len(ops)):
+                assert np.array_equal(_bits(outs[s][rd][k]), alone[k]), (s, rd, ops[k][0])
