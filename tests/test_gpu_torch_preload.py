@@ -297,3 +297,69 @@ def test_plain_ld_preload_random_products():
     err_lines = r.stderr.splitlines()
     assert not any("forwarding" in l for l in err_lines), [l for l in err_lines if "forwarding" in l][:5]
     assert sum(l.startswith("[vkblas] gemm ") for l in err_lines) >= 120, r.stderr[-2000:]
+
+
+# torch.cuda.graph under plain LD_PRELOAD: a step of products whose plans
+# need no partials (a 256-token linear on 64x64 tiles, 8-token and 1-token
+# decode linears, a 512^3 matmul) captured through the interposed
+# hipblasLtMatmul, replayed three times with eager steps between the
+# replays; every replay equals the eager step bit for bit.
+CHILD_GRAPH = r"""
+import json, torch
+dev = "cuda"
+torch.manual_seed(3)
+W1 = (torch.randn(1024, 1024, device=dev) * 0.03).half()
+W2 = (torch.randn(4096, 4096, device=dev) * 0.015).half()
+x1 = torch.randn(256, 1024, device=dev).half()
+x2 = torch.randn(8, 4096, device=dev).half()
+x3 = torch.randn(1, 4096, device=dev).half()
+a = torch.randn(512, 512, device=dev).half(); b = (torch.randn(512, 512, device=dev) * 0.05).half()
+def step():
+    return [x1 @ W1.t(), x2 @ W2.t(), x3 @ W2.t(), a @ b]
+eager = [t.clone() for t in step()]
+torch.cuda.synchronize()
+s = torch.cuda.Stream(); s.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(s):
+    for _ in range(2):
+        step()
+torch.cuda.current_stream().wait_stream(s)
+torch.cuda.synchronize()
+print("CAPTURE", flush=True)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    outs = step()
+res = []
+for rep in range(3):
+    for o in outs:
+        o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    res.append([bool(torch.equal(o, e)) for o, e in zip(outs, eager)])
+    again = step()
+    torch.cuda.synchronize()
+    res.append([bool(torch.equal(o, e)) for o, e in zip(again, eager)])
+print("RESULT " + json.dumps(res), flush=True)
+"""
+
+
+def test_plain_ld_preload_graph_capture_without_partials():
+    import os
+    import vkblas_amd as vk
+    # the step's calls, in the engine's row-major form, need no partials
+    for M, N, K in ((256, 1024, 1024), (8, 4096, 4096), (1, 4096, 4096)):
+        pl = vk.plan(vk.DT_F16, vk.DT_F16, 0, 1, M, N, K, K, K, N)
+        assert pl.split == 1 and pl.path not in (vk.PATH_SPLITK, vk.PATH_TAIL), (M, N, K, pl.path, pl.split)
+    pl = vk.plan(vk.DT_F16, vk.DT_F16, 0, 0, 512, 512, 512, 512, 512, 512)
+    assert pl.split == 1 and pl.path not in (vk.PATH_SPLITK, vk.PATH_TAIL)
+    old = os.environ.get("LD_PRELOAD", "")
+    env = dict(os.environ, LD_PRELOAD=":".join([vk.LIB_PATH] + ([old] if old else [])), VKBLAS_TRACE="1")
+    print("[case] plain LD_PRELOAD, torch.cuda.graph of products without partials", flush=True)
+    r = subprocess.run([sys.executable, "-c", CHILD_GRAPH], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    res = json.loads(next(l for l in r.stdout.splitlines() if l.startswith("RESULT "))[len("RESULT "):])
+    assert res and all(all(x) for x in res), res
+    err = r.stderr.splitlines()
+    assert not any("forwarding" in l for l in err), [l for l in err if "forwarding" in l][:5]
+    assert not any("declined" in l for l in err), [l for l in err if "declined" in l][:5]
+    assert sum(l.startswith("[vkblas] hipblaslt matmul") for l in err) >= 4 * 4, r.stderr[-2000:]
