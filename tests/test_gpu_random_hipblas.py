@@ -197,3 +197,76 @@ def test_random_hipblas(handle, c):
         assert np.all(np.isfinite(g)), f"batch {b}: non-finite output"
         err = normwise(g, w)
         assert err <= bound, f"batch {b}: normwise {err:.3g} > {bound:.3g}"
+
+
+# hipblasGemmEx type and compute codes: every fp32-compute code (32F, its
+# PEDANTIC and FAST_16F / FAST_16BF / FAST_TF32 forms: full fp32 arithmetic is
+# an allowed implementation of each), COMPUTE_16F with half scalars for
+# fp16 -> fp16, and the pre-3.0 hipblasDatatype_t values (150 = R_16F,
+# 151 = R_32F, 168 = R_16B, also as compute types) that the reference
+# accepted (src/vkblas_hipblas.c:280-284).  Each call computed here (the
+# marker call's path replaced) and checked against the oracle.
+COMPUTE = {"16F": 0, "32F": 2, "32F_PEDANTIC": 3, "32F_FAST_16F": 4, "32F_FAST_16BF": 5, "32F_FAST_TF32": 6,
+           "legacy_16F": 150, "legacy_32F": 151}
+MODERN = {"f32": 0, "f16": 2, "bf16": 14}
+LEGACY = {"f32": 151, "f16": 150, "bf16": 168}
+CT_CASES = []
+for comp in ("32F", "32F_PEDANTIC", "32F_FAST_16F", "32F_FAST_16BF", "32F_FAST_TF32", "legacy_32F"):
+    for ab, ct in (("f16", "f16"), ("f16", "f32"), ("bf16", "bf16"), ("bf16", "f32"), ("f32", "f32"),
+                   ("f32", "f16"), ("f32", "bf16")):
+        CT_CASES.append((ab, ct, comp, "modern"))
+    CT_CASES.append(("f16", "f16", comp, "legacy"))
+CT_CASES += [("f16", "f16", "16F", "modern"), ("f16", "f16", "16F", "legacy"), ("f16", "f16", "legacy_16F", "legacy"),
+             ("bf16", "bf16", "32F", "legacy"), ("bf16", "f32", "legacy_32F", "legacy"), ("f32", "f32", "32F", "legacy")]
+
+
+@pytest.mark.parametrize("case", CT_CASES, ids=lambda c: f"{c[0]}-{c[1]}_{c[2]}_{c[3]}")
+def test_gemmex_compute_and_type_codes(handle, case):
+    import torch
+    import vkblas_amd as vk
+    from vkblas_amd import hipblas_abi as hb
+    from gpu_helpers import normwise, f32_bound, F16_BOUND, BF16_BOUND
+    ab, ct, comp, enums = case
+    print(f"[case] gemmex codes {case}", flush=True)
+    codes = LEGACY if enums == "legacy" else MODERN
+    m, n, k, ta, tb = 296, 200, 264, 1, 0
+    r = np.random.default_rng(4242)
+    lda, ldb, ldc = k, k, m
+    A = _mats(r, 1, m * lda, m, k, lda, ab, 1.0)       # A stored k x m column-major (T): m rows of k
+    B = _mats(r, 1, n * ldb, n, k, ldb, ab, 0.05)      # B stored k x n column-major (N): n rows of k
+    C = _mats(r, 1, n * ldc, n, m, ldc, ct, 1.0)
+    TD = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}
+
+    def dev(x, t):
+        return torch.from_numpy(x.view(np.int16) if x.dtype == np.uint16 else x).view(TD[t]).to("cuda:0")
+    dA, dB, dC = dev(A, ab), dev(B, ab), dev(C, ct)
+    alpha, beta = 0.75, -0.5
+    if COMPUTE[comp] in (0, 150):   # half scalars
+        sa, sb = [ctypes.c_uint16(int(np.array([v], np.float16).view(np.uint16)[0])) for v in (alpha, beta)]
+    else:
+        sa, sb = ctypes.c_float(alpha), ctypes.c_float(beta)
+    dt = {"f32": vk.DT_F32, "f16": vk.DT_F16, "bf16": vk.DT_BF16}
+    pl = vk.plan(dt[ab], dt[ct], tb, ta, n, m, k, ldb, lda, ldc)
+    x = torch.zeros(65 * 64, dtype=torch.float16, device="cuda:0")
+    w = torch.zeros(64 * 64, dtype=torch.float16, device="cuda:0")
+    y = torch.zeros(65 * 64, dtype=torch.float16, device="cuda:0")
+    rows_mk = 2 if pl.path != vk.PATH_SKINNY else 65
+    vk.gemm_async(vk.DT_F16, vk.DT_F16, 0, 1 if rows_mk == 2 else 0, rows_mk, 64, 64, 1.0, x.data_ptr(), 64,
+                  w.data_ptr(), 64, 0.0, y.data_ptr(), 64)
+    torch.cuda.synchronize()
+    marker = vk.last_path()
+    handle.set_stream(torch.cuda.current_stream().cuda_stream)
+    st = handle.abi.hipblasGemmEx(handle.h, hb.HIPBLAS_OP_T, hb.HIPBLAS_OP_N, m, n, k, ctypes.byref(sa), dA.data_ptr(),
+                                  codes[ab], lda, dB.data_ptr(), codes[ab], ldb, ctypes.byref(sb), dC.data_ptr(),
+                                  codes[ct], ldc, COMPUTE[comp], hb.HIPBLAS_GEMM_DEFAULT)
+    torch.cuda.synchronize()
+    assert st == hb.HIPBLAS_STATUS_SUCCESS
+    assert vk.last_path() == pl.path != marker, "the call was forwarded"
+    got = dC.cpu()
+    got = got.view(torch.int16).numpy().view(np.uint16) if ct != "f32" else got.numpy()
+    want = C.copy()
+    oracle.ref_gemm_epi_rm(ab, ct, tb, ta, n, m, k, B, ldb, A, lda, alpha, beta, C.copy(), ldc, want, ldc, None)
+    bound = f32_bound(k) if (ab, ct) == ("f32", "f32") else (BF16_BOUND if ct == "bf16" else F16_BOUND)
+    g = BACK[ct](got.reshape(n, ldc)[:, :m])
+    wv = BACK[ct](want.reshape(n, ldc)[:, :m])
+    assert normwise(g, wv) <= bound
