@@ -1,7 +1,9 @@
 """The 64-bit-integer (_64) and _v2 forms of the intercepted hipBLAS and
 rocBLAS GEMM entry points: hipblasSgemm_64, hipblasHgemm_64, their strided
 batched forms, hipblasGemmEx_64 / _v2, hipblasGemmStridedBatchedEx_64 / _v2,
-rocblas_gemm_ex_64 and rocblas_gemm_strided_batched_ex_64.  Each call runs
+rocblas_gemm_ex_64, rocblas_gemm_strided_batched_ex_64, and the pointer-array
+batched hipblasSgemmBatched_64, hipblasHgemmBatched_64,
+hipblasGemmBatchedEx_64 and rocblas_gemm_batched_ex_64.  Each call runs
 on the same operands as its 32-bit form and must give the same bits (the
 same engine call), be computed by this library (a marker call on another
 path goes first: a forwarded call would leave the marker's path), and match
@@ -174,3 +176,83 @@ def test_64_and_v2_forms_match_32_bit_forms(ctx, entry):
         g = BACK[ct](outs[1][b * sc:(b + 1) * sc][: n * ldc].reshape(n, ldc)[:, :m])
         w = BACK[ct](want[: n * ldc].reshape(n, ldc)[:, :m])
         assert normwise(g, w) <= bound, b
+
+
+# Pointer-array batched forms: hipblasSgemmBatched_64, hipblasHgemmBatched_64,
+# hipblasGemmBatchedEx_64 and rocblas_gemm_batched_ex_64 against their 32-bit
+# forms (themselves checked against the oracle in test_gpu_batched_ptr.py and
+# test_gpu_rocblas.py), bitwise, each computed here.
+PSIGS = {
+    "hipblasSgemmBatched_64": [_vp, _i, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64],
+    "hipblasHgemmBatched_64": [_vp, _i, _i, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64],
+    "hipblasGemmBatchedEx_64": [_vp, _i, _i, _i64, _i64, _i64, _vp, _vp, _i, _i64, _vp, _i, _i64, _vp, _vp, _i, _i64,
+                                _i64, _i, _i],
+    "rocblas_gemm_batched_ex": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _i, _i, _vp, _vp, _i, _i, _vp, _i, _i,
+                                _i, _i, _i, ctypes.c_int32, _u32],
+    "rocblas_gemm_batched_ex_64": [_vp, _i, _i, _i64, _i64, _i64, _vp, _vp, _i, _i64, _vp, _i, _i64, _vp, _vp, _i,
+                                   _i64, _vp, _i, _i64, _i64, _i, _i, ctypes.c_int32, _u32],
+}
+PENTRIES = [("hipblasSgemmBatched_64", "hipblasSgemmBatched", "f32", "f32"),
+            ("hipblasHgemmBatched_64", "hipblasHgemmBatched", "f16", "f16"),
+            ("hipblasGemmBatchedEx_64", "hipblasGemmBatchedEx", "bf16", "f32"),
+            ("rocblas_gemm_batched_ex_64", "rocblas_gemm_batched_ex", "f16", "f16")]
+
+
+@pytest.mark.parametrize("entry", PENTRIES, ids=lambda e: e[0])
+def test_64_pointer_array_forms_match_32_bit_forms(ctx, entry):
+    vk = ctx.vk
+    for nm, args in PSIGS.items():
+        f = getattr(ctx.lib, nm)
+        f.argtypes = args
+        f.restype = _i
+    name, base, ab, ct = entry
+    print(f"[case] pointer-array entry {name} against {base}", flush=True)
+    m, n, k, nb = 200, 72, 136, 3
+    lda, ldb, ldc = k + 8, k, m + 8                   # A stored k x m (transA = T), B k x n (N)
+    r = np.random.default_rng(sum(map(ord, name)))
+
+    def dev(x, t):
+        return torch.from_numpy(x.view(np.int16) if x.dtype == np.uint16 else x).view(TD[t]).to("cuda:0")
+    As = [dev(CONV[ab]((r.standard_normal(m * lda) * 0.5).astype(np.float32)), ab) for _ in range(nb)]
+    Bs = [dev(CONV[ab]((r.standard_normal(n * ldb) * 0.05).astype(np.float32)), ab) for _ in range(nb)]
+    C0 = [CONV[ct](r.standard_normal(n * ldc).astype(np.float32)) for _ in range(nb)]
+    pA = torch.tensor([t.data_ptr() for t in As], dtype=torch.int64, device="cuda:0")
+    pB = torch.tensor([t.data_ptr() for t in Bs], dtype=torch.int64, device="cuda:0")
+    alpha, beta = 0.75, 0.5
+    half = name.startswith("hipblasH")
+    if half:
+        sa_, sb_ = [ctypes.c_uint16(int(np.array([v], np.float16).view(np.uint16)[0])) for v in (alpha, beta)]
+    else:
+        sa_, sb_ = ctypes.c_float(alpha), ctypes.c_float(beta)
+    outs = []
+    for fn in (base, name):
+        Cs = [dev(c, ct) for c in C0]
+        pC = torch.tensor([t.data_ptr() for t in Cs], dtype=torch.int64, device="cuda:0")
+        marker = _marker(vk, vk.PATH_TILE64)        # pointer arrays run the checked 64x64 kernel
+        h = ctx.hip.h
+        if fn in ("hipblasSgemmBatched", "hipblasHgemmBatched"):
+            st = getattr(ctx.hip.abi, fn)(h, OPT, OPN, m, n, k, ctypes.byref(sa_), pA.data_ptr(), lda,
+                                          pB.data_ptr(), ldb, ctypes.byref(sb_), pC.data_ptr(), ldc, nb)
+        elif fn in ("hipblasSgemmBatched_64", "hipblasHgemmBatched_64"):
+            st = getattr(ctx.lib, fn)(h, OPT, OPN, m, n, k, ctypes.byref(sa_), pA.data_ptr(), lda, pB.data_ptr(), ldb,
+                                      ctypes.byref(sb_), pC.data_ptr(), ldc, nb)
+        elif fn == "hipblasGemmBatchedEx":
+            st = ctx.hip.abi.hipblasGemmBatchedEx(h, OPT, OPN, m, n, k, ctypes.byref(sa_), pA.data_ptr(), HT[ab], lda,
+                                                  pB.data_ptr(), HT[ab], ldb, ctypes.byref(sb_), pC.data_ptr(),
+                                                  HT[ct], ldc, nb, 2, 160)
+        elif fn == "hipblasGemmBatchedEx_64":
+            st = ctx.lib.hipblasGemmBatchedEx_64(h, OPT, OPN, m, n, k, ctypes.byref(sa_), pA.data_ptr(), HT[ab], lda,
+                                                 pB.data_ptr(), HT[ab], ldb, ctypes.byref(sb_), pC.data_ptr(), HT[ct],
+                                                 ldc, nb, 2, 160)
+        else:
+            st = getattr(ctx.lib, fn)(ctx.rh, OPT, OPN, m, n, k, ctypes.byref(sa_), pA.data_ptr(), RT[ab], lda,
+                                      pB.data_ptr(), RT[ab], ldb, ctypes.byref(sb_), pC.data_ptr(), RT[ct], ldc,
+                                      pC.data_ptr(), RT[ct], ldc, nb, 151, 0, 0, 0)
+        torch.cuda.synchronize()
+        assert st == 0, (fn, st)
+        # the marker left PATH_SKINNY: a forwarded call would not replace it
+        assert marker == vk.PATH_SKINNY
+        assert vk.last_path() == vk.PATH_TILE64 and vk.last_kernel() == vk.KERNEL_GENERIC_CHECKED, (fn, vk.last_path())
+        outs.append([c.cpu().view(torch.int16 if ct != "f32" else torch.int32).numpy().copy() for c in Cs])
+    for b in range(nb):
+        assert np.array_equal(outs[0][b], outs[1][b]), f"{name} differs from {base}, batch {b}"
