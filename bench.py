@@ -360,7 +360,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the GEMM hot path has no multi-GPU path in this build "
-              "(see DESIGN.md for how it would shard). Run with --gpus 1.", file=sys.stderr)
+              "(each GPU would run its own GEMMs on its own stream). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -536,8 +536,9 @@ def vendor(torch, vk, stream, steps):
     gfx950), timed like the vkblas legs: fp32 / fp16 / bf16 4096^3 (row-major
     a @ b and a @ b.t(), i.e. hipBLAS NN and TN), the `shapes` leg's GEMMs
     (a @ b) and 8192x8192 fp16 decode x @ w.t() and x @ w with three weight
-    copies rotated.  Not part of the default run: the comparison in DESIGN.md comes
-    from here (plain, and with libvkblas_hipblas.so under LD_PRELOAD)."""
+    copies rotated.  Not part of the default run: the library-against-vendor
+    comparison is run from here (plain, and with libvkblas_hipblas.so under
+    LD_PRELOAD)."""
     n = 4096
     g = torch.Generator(device="cuda:0").manual_seed(7)
     out = {}
