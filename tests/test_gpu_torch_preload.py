@@ -184,7 +184,7 @@ print("RESULT " + json.dumps(out), flush=True)
 
 def test_plain_ld_preload_reference_script():
     """LD_PRELOAD=libvkblas_hipblas.so python script.py, the reference's
-    usage (README.md:60-70), with its test_torch.py cases: every fp32 / fp16
+    usage (reference README.md:60-70), with its test_torch.py cases: every fp32 / fp16
     / bf16 product reaches this library through hipblasLtMatmul (bias
     epilogues included) and matches PyTorch's CPU result; complex128 goes to
     the vendor library and is exact to 1e-8 as the reference requires."""
