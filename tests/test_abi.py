@@ -127,6 +127,11 @@ def test_plan_rejects_bad_arguments():
         P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 4, 8, 0, 8, 4)          # lda == 0
     with pytest.raises(vk.VkblasError):
         P(vk.DT_F32, vk.DT_F32, 0, 0, 4, 8, 4, 4, 8, 0)          # ldc == 0
+    # dimensions past the kernels' 32-bit signed indices: declined
+    for M, N, K in ((1 << 31, 4, 4), (4, 1 << 31, 4), (4, 4, 1 << 31), (0xFFFFFFFF, 1, 1)):
+        with pytest.raises(vk.VkblasError):
+            P(vk.DT_F16, vk.DT_F16, 0, 0, M, N, K, K, N, N)
+    assert P(vk.DT_F16, vk.DT_F16, 0, 0, (1 << 31) - 1, 1, 1, 1, 1, 1).path != vk.PATH_NONE
     # the engine contract takes leading dimensions as given (reference
     # test/test_h.c:105 passes lda = K + M%2 < M with op_a = T)
     assert P(vk.DT_F16, vk.DT_F16, 1, 0, 8, 4, 6, 6, 4, 4).path != vk.PATH_NONE

@@ -397,6 +397,10 @@ vkblas_status_t vkblas_plan_gemm(vkblas_dtype_t ab_type, vkblas_dtype_t c_type,
     if (!plan) return VKBLAS_ERR_PARAM;
     memset(plan, 0, sizeof(*plan));
     if (M == 0 || N == 0 || K == 0 || batch == 0) return VKBLAS_ERR_PARAM;
+    /* the kernels index rows, columns and k with 32-bit signed integers (their
+     * pointer arithmetic is 64-bit); larger dimensions are declined, and the
+     * hipBLAS / rocBLAS / hipBLASLt entry points forward such calls */
+    if (M > 0x7fffffffu || N > 0x7fffffffu || K > 0x7fffffffu) return VKBLAS_ERR_PARAM;
     if (!((ab_type == VKBLAS_DT_F32 && (c_type == VKBLAS_DT_F32 || c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_BF16)) ||
           (ab_type == VKBLAS_DT_F16 && (c_type == VKBLAS_DT_F16 || c_type == VKBLAS_DT_F32)) ||
           (ab_type == VKBLAS_DT_BF16 && (c_type == VKBLAS_DT_BF16 || c_type == VKBLAS_DT_F32))))
